@@ -1,0 +1,265 @@
+// cx_device.hpp -- device building blocks for the gfx950 sampling kernels.
+//
+// Workgroups are 1024 threads = 16 wave64s.  Everything here is written for
+// 64-lane wavefronts: ballots are 64-bit, lane prefix counts use mbcnt, and
+// sub-wave exchanges use cross-lane shuffles (ds_swizzle / DPP / bpermute).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <limits.h>
+
+namespace cx {
+
+constexpr int WG = 1024;
+constexpr int NWAVE = WG / 64;
+
+// ------------------------------------------------------------ orderable keys
+// Map a float to an unsigned integer whose unsigned order is the float order
+// (-inf < ... < -0 < +0 < ... < +inf).  0 is below every float and serves as
+// "no element".
+__device__ __forceinline__ uint32_t f2key(float f) {
+  uint32_t b = __float_as_uint(f);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+__device__ __forceinline__ float key2f(uint32_t k) {
+  uint32_t b = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+  return __uint_as_float(b);
+}
+__device__ __forceinline__ uint64_t d2key(double d) {
+  uint64_t b = (uint64_t)__double_as_longlong(d);
+  return (b >> 63) ? ~b : (b | (1ull << 63));
+}
+__device__ __forceinline__ double key2d(uint64_t k) {
+  uint64_t b = (k >> 63) ? (k & 0x7fffffffffffffffull) : ~k;
+  return __longlong_as_double((long long)b);
+}
+
+// ------------------------------------------------------------ lanes
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+__device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
+__device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }
+__device__ __forceinline__ int lanes_below(uint64_t m) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                   __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+template <typename T>
+__device__ __forceinline__ T uniform(T v) {  // value of the first active lane
+  return __shfl(v, __builtin_ctzll(__ballot(1)));
+}
+
+template <typename T> __device__ __forceinline__ T wave_max(T v) {
+  for (int o = 32; o > 0; o >>= 1) { T w = __shfl_xor(v, o); v = w > v ? w : v; }
+  return v;
+}
+template <typename T> __device__ __forceinline__ T wave_min(T v) {
+  for (int o = 32; o > 0; o >>= 1) { T w = __shfl_xor(v, o); v = w < v ? w : v; }
+  return v;
+}
+template <typename T> __device__ __forceinline__ T wave_sum(T v) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+// (value, index) argmax with NumPy's rule: larger value wins, equal values go
+// to the lower index.  NaN is handled separately by the callers.
+__device__ __forceinline__ void argmax_merge(double& v, int& i, double w, int j) {
+  if (w > v || (w == v && j < i)) { v = w; i = j; }
+}
+__device__ __forceinline__ void wave_argmax(double& v, int& i) {
+  for (int o = 32; o > 0; o >>= 1) {
+    double w = __shfl_xor(v, o);
+    int j = __shfl_xor(i, o);
+    argmax_merge(v, i, w, j);
+  }
+}
+
+// Block-wide reductions through a small LDS scratch (>= NWAVE slots).
+template <typename T>
+__device__ __forceinline__ T block_sum(T v, T* scratch) {
+  v = wave_sum(v);
+  if (lane_id() == 0) scratch[wave_id()] = v;
+  __syncthreads();
+  T r = 0;
+  if (threadIdx.x < 64) {
+    r = threadIdx.x < NWAVE ? scratch[threadIdx.x] : T(0);
+    r = wave_sum(r);
+    if (threadIdx.x == 0) scratch[0] = r;
+  }
+  __syncthreads();
+  r = scratch[0];
+  __syncthreads();
+  return r;
+}
+template <typename T>
+__device__ __forceinline__ T block_max(T v, T* scratch, T lowest) {
+  v = wave_max(v);
+  if (lane_id() == 0) scratch[wave_id()] = v;
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    T r = threadIdx.x < NWAVE ? scratch[threadIdx.x] : lowest;
+    r = wave_max(r);
+    if (threadIdx.x == 0) scratch[0] = r;
+  }
+  __syncthreads();
+  T r = scratch[0];
+  __syncthreads();
+  return r;
+}
+template <typename T>
+__device__ __forceinline__ T block_min(T v, T* scratch, T highest) {
+  v = wave_min(v);
+  if (lane_id() == 0) scratch[wave_id()] = v;
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    T r = threadIdx.x < NWAVE ? scratch[threadIdx.x] : highest;
+    r = wave_min(r);
+    if (threadIdx.x == 0) scratch[0] = r;
+  }
+  __syncthreads();
+  T r = scratch[0];
+  __syncthreads();
+  return r;
+}
+__device__ __forceinline__ void block_argmax(double& v, int& i, double* sv, int* si) {
+  wave_argmax(v, i);
+  if (lane_id() == 0) { sv[wave_id()] = v; si[wave_id()] = i; }
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    double w = threadIdx.x < NWAVE ? sv[threadIdx.x] : -__builtin_inf();
+    int j = threadIdx.x < NWAVE ? si[threadIdx.x] : INT_MAX;
+    wave_argmax(w, j);
+    if (threadIdx.x == 0) { sv[0] = w; si[0] = j; }
+  }
+  __syncthreads();
+  v = sv[0];
+  i = si[0];
+  __syncthreads();
+}
+
+// ------------------------------------------------------------ sort records
+// A record orders by key descending, then by idx ascending (NumPy's stable
+// tie rule: equal probabilities keep the lower token id first).
+struct Rec {
+  uint64_t key;
+  int32_t idx;
+  int32_t aux;
+};
+__device__ __forceinline__ bool rec_before(const Rec& a, const Rec& b) {
+  return a.key > b.key || (a.key == b.key && a.idx < b.idx);
+}
+__device__ __forceinline__ Rec shfl_xor_rec(const Rec& r, int o) {
+  Rec s;
+  s.key = __shfl_xor(r.key, o);
+  s.idx = __shfl_xor(r.idx, o);
+  s.aux = __shfl_xor(r.aux, o);
+  return s;
+}
+// One compare-exchange of element e (held in r) with element e ^ stride
+// (held in p) inside a bitonic merge of blocks of `size`.
+__device__ __forceinline__ Rec bitonic_pick(const Rec& r, const Rec& p, int e, int stride,
+                                            int size) {
+  bool lower = (e & stride) == 0;
+  bool first_half_desc = (e & size) == 0;
+  bool want_first = (lower == first_half_desc);
+  bool r_first = rec_before(r, p);
+  return (want_first == r_first) ? r : p;
+}
+
+// Sort n <= 2 * WG records held in LDS (k, i, a) into rec_before order.
+// Thread t owns elements t and t + WG.  Strides below 64 exchange through
+// cross-lane shuffles, larger strides through LDS.
+__device__ inline void block_sort(uint64_t* k, int32_t* i, int32_t* a, int n) {
+  int np = 2;
+  while (np < n) np <<= 1;
+  const int t = threadIdx.x;
+  for (int e = n + t; e < np; e += WG) { k[e] = 0; i[e] = INT_MAX; a[e] = -1; }
+  __syncthreads();
+  if (np <= 64) {
+    if (t < 64) {
+      Rec r;
+      bool have = t < np;
+      r.key = have ? k[t] : 0;
+      r.idx = have ? i[t] : INT_MAX;
+      r.aux = have ? a[t] : -1;
+      for (int size = 2; size <= np; size <<= 1)
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+          Rec p = shfl_xor_rec(r, stride);
+          r = bitonic_pick(r, p, t, stride, size);
+        }
+      if (have) { k[t] = r.key; i[t] = r.idx; a[t] = r.aux; }
+    }
+    __syncthreads();
+    return;
+  }
+  const bool two = np > WG;
+  Rec r0, r1;
+  r0.key = t < np ? k[t] : 0; r0.idx = t < np ? i[t] : INT_MAX; r0.aux = t < np ? a[t] : -1;
+  if (two) { r1.key = k[t + WG]; r1.idx = i[t + WG]; r1.aux = a[t + WG]; }
+  __syncthreads();
+  for (int size = 2; size <= np; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      if (stride >= WG) {                       // partner is the thread's other element
+        Rec lo = bitonic_pick(r0, r1, t, stride, size);
+        Rec hi = bitonic_pick(r1, r0, t + WG, stride, size);
+        r0 = lo; r1 = hi;
+      } else if (stride >= 64) {                // partner in another wave: via LDS
+        if (t < np) { k[t] = r0.key; i[t] = r0.idx; a[t] = r0.aux; }
+        if (two) { k[t + WG] = r1.key; i[t + WG] = r1.idx; a[t + WG] = r1.aux; }
+        __syncthreads();
+        if (t < np) {
+          int q = t ^ stride;
+          Rec p; p.key = k[q]; p.idx = i[q]; p.aux = a[q];
+          r0 = bitonic_pick(r0, p, t, stride, size);
+        }
+        if (two) {
+          int q = (t + WG) ^ stride;
+          Rec p; p.key = k[q]; p.idx = i[q]; p.aux = a[q];
+          r1 = bitonic_pick(r1, p, t + WG, stride, size);
+        }
+        __syncthreads();
+      } else {                                  // same wave: shuffles
+        Rec p0 = shfl_xor_rec(r0, stride);
+        r0 = bitonic_pick(r0, p0, t, stride, size);
+        if (two) {
+          Rec p1 = shfl_xor_rec(r1, stride);
+          r1 = bitonic_pick(r1, p1, t + WG, stride, size);
+        }
+      }
+    }
+  }
+  if (t < np) { k[t] = r0.key; i[t] = r0.idx; a[t] = r0.aux; }
+  if (two) { k[t + WG] = r1.key; i[t + WG] = r1.idx; a[t + WG] = r1.aux; }
+  __syncthreads();
+}
+
+// Inclusive prefix sum of v[0..n), n <= 2 * WG, in place (fp64).  Thread t
+// owns elements 2t and 2t+1.
+__device__ inline void block_scan(double* v, int n, double* scratch) {
+  const int t = threadIdx.x;
+  double a = 2 * t < n ? v[2 * t] : 0.0;
+  double b = 2 * t + 1 < n ? v[2 * t + 1] : 0.0;
+  double s = a + b;
+  double inc = s;                                // inclusive scan across the wave
+  for (int o = 1; o < 64; o <<= 1) {
+    double w = __shfl_up(inc, o);
+    if (lane_id() >= o) inc += w;
+  }
+  if (lane_id() == 63) scratch[wave_id()] = inc;
+  __syncthreads();
+  if (t < 64) {
+    double w = t < NWAVE ? scratch[t] : 0.0;
+    double x = w;
+    for (int o = 1; o < 64; o <<= 1) {
+      double y = __shfl_up(x, o);
+      if (t >= o) x += y;
+    }
+    if (t < NWAVE) scratch[NWAVE + t] = x - w;   // exclusive wave offsets
+  }
+  __syncthreads();
+  double base = scratch[NWAVE + wave_id()] + (inc - s);
+  if (2 * t < n) v[2 * t] = base + a;
+  if (2 * t + 1 < n) v[2 * t + 1] = base + a + b;
+  __syncthreads();
+}
+
+}  // namespace cx

@@ -1,0 +1,148 @@
+// cx_internal.hpp -- layouts shared by the host entry points and the kernels.
+#pragma once
+#include <stdint.h>
+#include <stddef.h>
+#include "cx_sampler.h"
+
+namespace cx {
+
+constexpr int CAPW = 256;                 // per-wave candidate buffer (entries)
+constexpr int KW_MAX = 128;               // entries a wave keeps when it compacts
+constexpr int SORT_CAP = 2048;            // finisher sort capacity (2 per thread)
+constexpr int WIN_MAX = 4095;             // longest penalty window held in LDS
+constexpr int CAPS = 16 * CAPW + 4096;    // candidates per (row, slice) in the workspace
+constexpr uint32_t HEMPTY = 0xFFFFFFFFu;  // empty hash slot
+constexpr double TOL_S = 4e-6;            // relative error bound of the fp32-term normaliser
+
+// SplitStats.flags
+constexpr int SF_OVERFLOW = 1;            // a wave buffer flooded with ties
+constexpr int SF_UNSUPPORTED = 2;         // window longer than WIN_MAX
+
+// Internal row_status value: the finisher could not decide the row and the
+// multi-pass kernel must finish it.  Never returned to the caller.
+constexpr int ROW_PENDING = 0x40000000;
+
+struct SplitStats {       // one per (row, slice), 64 bytes
+  double m;               // max of the slice's penalised values (stochastic rows)
+  double s;               // sum of exp((x - m) / T) over the slice
+  double best_v;          // first maximum (greedy rows)
+  double pad0;
+  int32_t best_i;         // its index (INT_MAX if none)
+  int32_t nan_i;          // first NaN index (INT_MAX if none)
+  uint32_t tau;           // region threshold key; <= 1 means the region is the whole slice
+  int32_t ncand;          // region entries written to the workspace
+  int32_t flags;
+  int32_t pad1[3];
+};
+static_assert(sizeof(SplitStats) == 64, "SplitStats layout");
+
+struct Cand {             // 16 bytes
+  uint64_t key;           // orderable key of the fp64 (penalised) value
+  int32_t idx;
+  int32_t pad;
+};
+
+struct SampleArgs {
+  const void* logits;
+  int64_t ld;
+  int32_t B, V;
+  const int32_t* hist;
+  const int32_t* hist_len;
+  int64_t ldh;
+  const cx_row_params* prm;
+  const double* u;
+  int32_t* out_id;
+  int32_t* row_status;
+  float* out_probs;
+  int32_t* counters;      // [B], zero between calls
+  SplitStats* stats;      // [B * nsplit]
+  Cand* cands;            // [B * nsplit * CAPS]
+  int32_t nsplit, split_len;
+  int32_t ns, ns_log2;    // hash slots (power of two) and log2
+  int32_t nbw;            // bitmap words (power of two)
+  int32_t vec_ok;         // rows are 16-byte aligned
+  int32_t off_bitmap, off_hkey, off_hval, off_wkey, off_widx;
+  int32_t lds_bytes;
+  int32_t bf16;
+  int32_t slow_nbw;       // multi-pass kernel: full-row bitmap words (power of two)
+  int32_t slow_off_hkey, slow_off_work, slow_lds_bytes;
+};
+
+// ---------------------------------------------------------------- verify
+constexpr int VCHUNK = 32768;          // elements per verify stats / residual chunk
+
+struct ChunkStats {                    // 32 bytes per (row, chunk)
+  float m;                             // chunk max of x (stochastic rows)
+  float bv;                            // first max (greedy rows)
+  int32_t bi;
+  int32_t nan_i;
+  double s;                            // sum exp2((x - m) * c)
+  double pad;
+};
+
+struct SeqState {                      // 64 bytes per sequence
+  int32_t accepted, next_tok, used, status;
+  int32_t rej;                         // rejected position, -1 if none
+  int32_t exact;                       // normalisers below are exact fp64
+  float Mt, Mq;                        // row maxima of x at position rej
+  double St, Sq;                       // normalisers at position rej
+  double R, pad;
+};
+
+struct VerifyArgs {
+  const float* target;
+  const float* draft;
+  const int32_t* draft_ids;
+  const double* u;
+  const float* temperature;
+  int32_t B, gamma, V, nchunk;
+  int32_t* accepted;
+  int32_t* next_tok;
+  int32_t* used;
+  int32_t* row_status;
+  ChunkStats* cstats;                  // [(B*(gamma+1) + B*gamma) * nchunk]
+  SeqState* seq;                       // [B]
+  double* rmass;                       // [B * nchunk]
+};
+
+// Workspace layout (bytes), identical on host and device.
+struct SampleWorkspace {
+  size_t off_counters, off_stats, off_cands, total;
+};
+
+inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+inline int choose_nsplit(int B, int V) {
+  int by_rows = B >= 512 ? 1 : 512 / (B > 0 ? B : 1);
+  int by_len = V / 16384 > 0 ? V / 16384 : 1;
+  int n = by_rows < by_len ? by_rows : by_len;
+  if (n > 8) n = 8;
+  return n < 1 ? 1 : n;
+}
+
+struct VerifyWorkspace {
+  size_t off_cstats, off_seq, off_rmass, total;
+};
+
+inline VerifyWorkspace verify_workspace_layout(int B, int gamma, int V) {
+  VerifyWorkspace w;
+  int nchunk = (V + VCHUNK - 1) / VCHUNK;
+  size_t rows = (size_t)B * (gamma + 1) + (size_t)B * gamma;
+  w.off_cstats = 0;
+  w.off_seq = align_up(rows * nchunk * sizeof(ChunkStats), 256);
+  w.off_rmass = align_up(w.off_seq + (size_t)B * sizeof(SeqState), 256);
+  w.total = align_up(w.off_rmass + (size_t)B * nchunk * sizeof(double), 256);
+  return w;
+}
+
+inline SampleWorkspace sample_workspace_layout(int B, int V) {
+  SampleWorkspace w;
+  int ns = choose_nsplit(B, V);
+  w.off_counters = 0;
+  w.off_stats = align_up((size_t)B * 4, 256);
+  w.off_cands = align_up(w.off_stats + (size_t)B * ns * sizeof(SplitStats), 256);
+  w.total = align_up(w.off_cands + (size_t)B * ns * CAPS * sizeof(Cand), 256);
+  return w;
+}
+
+}  // namespace cx

@@ -1,0 +1,175 @@
+"""Sampler parity on the GPU: the HIP library against the oracle on the same
+inputs and uniforms (rules in tests/parity.py)."""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+
+import cases
+from chenxing_amd import workloads as W
+from chenxing_amd._lib import FLAG_SLOW, ROW_UNSUPPORTED, sample_host
+from chenxing_amd.params import RowParams
+from oracle import sampler_ref as R
+from parity import Tally, compare_rows, oracle_rows
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def _run(w, want_probs=True, rows=None):
+    _say(f"[gpu] sample {w.name} B={w.B} V={w.V} dtype={w.dtype}")
+    ids, st, probs = sample_host(w.logits, w.params, w.hist if w.hist.size else None,
+                                 w.hist_len, w.u, bf16=(w.dtype == "bf16"), want_probs=want_probs)
+    return ids, st, probs
+
+
+def _check(w, ids, st, probs, rows=None):
+    rows = list(range(w.B)) if rows is None else rows
+    orc = oracle_rows(w, rows)
+    t = compare_rows(ids[rows], st[rows], None if probs is None else probs[rows], orc, w.name)
+    assert not t.mismatches, t.mismatches[:5]
+    return t
+
+
+def test_small_batch_config():
+    w = W.small_batch()
+    ids, st, probs = _run(w)
+    t = _check(w, ids, st, probs)
+    assert t.draws == 4
+
+
+def test_full_penalty_config():
+    w = W.full_penalty()
+    ids, st, probs = _run(w)
+    t = _check(w, ids, st, probs)
+    assert t.draws == 256 and t.boundary == 0
+
+
+@pytest.mark.parametrize("greedy", [True, False])
+def test_nucleus_config(greedy):
+    w = W.nucleus(greedy=greedy)
+    ids, st, probs = _run(w)
+    t = _check(w, ids, st, probs)
+    assert t.rows == 64
+
+
+def test_hetero_bf16_config_subset():
+    w = W.hetero_bf16(B=96)
+    ids, st, probs = _run(w)
+    _check(w, ids, st, probs)
+
+
+def test_golden_small_rows():
+    """Every small golden case (all knobs, ties, -inf, NaN, underflow) through
+    the device, one batch per vocabulary size."""
+    all_cases = cases.small_sampler_cases()
+    by_v: dict = {}
+    for c in all_cases:
+        by_v.setdefault(c.logits.size, []).append(c)
+    total = Tally()
+    for V, cs in sorted(by_v.items()):
+        B = len(cs)
+        x = np.stack([c.logits for c in cs])
+        prm = [RowParams(temperature=c.params["temperature"], top_k=c.params["top_k"],
+                         top_p=c.params["top_p"], min_p=c.params["min_p"],
+                         typical_p=c.params["typical_p"],
+                         repetition_penalty=c.params["repetition_penalty"],
+                         n_keep=c.params["n_keep"]) for c in cs]
+        H = max(1, max(len(c.hist) for c in cs))
+        hist = np.full((B, H), -1, np.int32)
+        hl = np.zeros(B, np.int32)
+        for b, c in enumerate(cs):
+            hist[b, :len(c.hist)] = c.hist
+            hl[b] = len(c.hist)
+        u = np.array([np.random.default_rng(c.params["seed"]).random() for c in cs])
+        _say(f"[gpu] golden small rows V={V} B={B}")
+        ids, st, probs = sample_host(x, prm, hist, hl, u, want_probs=True)
+        orc = [R.sample_row(c.logits, p, c.hist, u[b], tie="stable", keep_probs=True)
+               for b, (c, p) in enumerate(zip(cs, prm))]
+        total.merge(compare_rows(ids, st, probs, orc, f"V{V}"))
+    assert not total.mismatches, total.mismatches[:5]
+
+
+def _slow_batch(V=50000, seed=3):
+    """Rows built to leave the fused path: each needs the multi-pass kernel."""
+    rng = np.random.default_rng(seed)
+    rows, prms = [], []
+
+    def add(x, **kw):
+        rows.append(np.asarray(x, np.float32))
+        prms.append(RowParams(**kw))
+
+    add(rng.normal(0, 0.5, V), temperature=1.0, top_p=0.9)            # deep nucleus
+    add(rng.normal(0, 2, V), temperature=0.8, top_k=5000)             # k beyond the region
+    add(np.zeros(V), temperature=1.0, top_k=10)                       # one tie group
+    q = np.round(rng.normal(0, 1, V) * 4) / 4                          # coarse ties
+    add(q, temperature=1.0, top_p=0.6)
+    add(rng.normal(0, 1, V), temperature=1.0, min_p=0.01)             # wide min-p
+    add(rng.normal(0, 2, V), temperature=1.0, typical_p=0.8)          # typical-p
+    add(rng.normal(0, 2, V), temperature=0.9, top_k=100, typical_p=0.5)
+    bad = rng.normal(0, 2, V)
+    bad[123] = np.nan
+    add(bad, temperature=1.0, top_k=5)                                 # NaN -> argmax
+    add(bad, temperature=1.0)                                          # NaN -> error
+    inf = rng.normal(0, 2, V)
+    inf[77] = np.inf
+    add(inf, temperature=1.0, min_p=0.1)                               # +inf -> argmax
+    add(np.full(V, -np.inf), temperature=1.0)                          # all -inf -> error
+    add(rng.normal(0, 0.1, V), temperature=0.001, top_k=3)             # underflow -> argmax
+    add(rng.normal(0, 0.1, V), temperature=0.001)                      # underflow -> error
+    add(rng.normal(0, 1, V), temperature=1.3, top_p=0.999)            # nucleus ~ all
+    return np.stack(rows), prms
+
+
+def test_slow_path_rows():
+    x, prm = _slow_batch()
+    B = x.shape[0]
+    u = np.random.default_rng(11).random(B)
+    _say(f"[gpu] slow-path rows B={B} V={x.shape[1]}")
+    ids, st, probs = sample_host(x, prm, None, None, u, want_probs=True)
+    orc = [R.sample_row(x[b], prm[b], None, u[b], tie="stable", keep_probs=True)
+           for b in range(B)]
+    t = compare_rows(ids, st, probs, orc, "slow")
+    assert not t.mismatches, t.mismatches[:5]
+    assert all(int(s) & FLAG_SLOW for s in st[:7])
+
+
+def test_penalties_long_window_and_unaligned_rows():
+    """Penalty windows with n_keep, duplicates and out-of-range ids; a row
+    stride that breaks 16-byte alignment (scalar path)."""
+    rng = np.random.default_rng(5)
+    B, V, H = 24, 30001, 3000
+    x = rng.normal(0, 2, (B, V)).astype(np.float32)
+    hist = rng.integers(-50, V + 50, (B, H)).astype(np.int32)
+    hl = rng.integers(0, H + 1, B).astype(np.int32)
+    prm = [RowParams(temperature=float(rng.choice([0.0, 0.6, 1.0])), top_k=int(rng.choice([0, 7])),
+                     top_p=float(rng.choice([1.0, 0.8])), repetition_penalty=float(rng.choice([1.0, 1.3])),
+                     presence_penalty=float(rng.choice([0.0, 0.4])),
+                     frequency_penalty=float(rng.choice([0.0, 0.2])),
+                     n_keep=int(rng.choice([0, 100, 2000]))) for _ in range(B)]
+    u = rng.random(B)
+    _say(f"[gpu] penalties B={B} V={V} H={H}")
+    ids, st, probs = sample_host(x, prm, hist, hl, u, want_probs=True)
+    lists = R.hist_rows_to_lists(hist, hl)
+    orc = [R.sample_row(x[b], prm[b], lists[b], u[b], tie="stable", keep_probs=True)
+           for b in range(B)]
+    t = compare_rows(ids, st, probs, orc, "penalties")
+    assert not t.mismatches, t.mismatches[:5]
+
+
+def test_window_beyond_lds_limit_is_reported():
+    rng = np.random.default_rng(6)
+    B, V, H = 2, 5000, 5000
+    x = rng.normal(0, 1, (B, V)).astype(np.float32)
+    hist = rng.integers(0, V, (B, H)).astype(np.int32)
+    prm = [RowParams(repetition_penalty=1.2), RowParams(repetition_penalty=1.2, n_keep=100)]
+    _say("[gpu] window limit")
+    ids, st, _ = sample_host(x, prm, hist, np.full(B, H, np.int32), np.full(B, 0.5))
+    assert int(st[0]) & 0xFF == ROW_UNSUPPORTED       # 5000-id window
+    assert int(st[1]) & 0xFF != ROW_UNSUPPORTED       # last max(64, 100) ids only
