@@ -1,0 +1,244 @@
+#!/usr/bin/env python3
+"""Benchmark of the token-sampling hot path on one MI355X.
+
+Headline: the fused sampler on the full-penalty workload -- B=256 rows,
+V=128256 fp32 logits, 2048-id Zipf(1.1) histories, repetition 1.1 /
+presence 0.5 / frequency 0.3, T 0.7, top-k 40, top-p 0.9 -- with every input
+already resident in HBM.  A step is one cx_sample_f32 call over the batch.
+
+  value        sampled rows/s over exactly `--steps` timed steps
+  roofline     algorithmic bytes of one launch / the fused kernel's mean
+               duration (hipEvent pairs the library records around each
+               launch on its own stream), against 8 TB/s
+  cpu_baseline the NumPy oracle on the host, one core, on a bounded sample
+               of the same rows (reported beside, not a target)
+
+The other workloads (nucleus, speculative verify, heterogeneous bf16) are
+timed the same way and reported under "other_workloads".
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, HERE)
+
+HBM_PEAK_GBPS = 8000.0
+METRIC = "sampled rows/sec + achieved HBM GB/s, B=256 V=128256 penalties+top-k+top-p"
+
+
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def _say(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+class DeviceSample:
+    """A SampleWorkload uploaded to the GPU, ready for repeated calls."""
+
+    def __init__(self, w, dev):
+        import torch
+        from chenxing_amd.params import pack_rows
+        self.w = w
+        if w.dtype == "bf16":
+            self.x = torch.from_numpy(w.logits.view(np.int16)).to(dev).view(torch.bfloat16)
+        else:
+            self.x = torch.from_numpy(w.logits).to(dev)
+        self.prm = torch.from_numpy(pack_rows(w.params).view(np.uint8)).to(dev)
+        self.u = torch.from_numpy(w.u).to(dev)
+        self.h = torch.from_numpy(w.hist).to(dev) if w.hist.size else None
+        self.hl = torch.from_numpy(w.hist_len).to(dev) if w.hist.size else None
+        self.ids = torch.empty(w.B, dtype=torch.int32, device=dev)
+        self.st = torch.empty(w.B, dtype=torch.int32, device=dev)
+
+    def __call__(self):
+        from chenxing_amd import _lib
+        _lib.sample_device(self.x, self.prm, self.u, self.h, self.hl, self.ids, self.st)
+
+
+class DeviceVerify:
+    def __init__(self, w, dev):
+        import torch
+        self.w = w
+        self.t = torch.from_numpy(w.target).to(dev)
+        self.d = torch.from_numpy(w.draft).to(dev)
+        self.ids = torch.from_numpy(w.draft_ids).to(dev)
+        self.u = torch.from_numpy(w.u).to(dev)
+        self.T = torch.from_numpy(w.temperature).to(dev)
+        B = w.target.shape[0]
+        self.out = [torch.empty(B, dtype=torch.int32, device=dev) for _ in range(4)]
+
+    def __call__(self):
+        from chenxing_amd import _lib
+        _lib.spec_verify_device(self.t, self.d, self.ids, self.u, self.T, *self.out)
+
+
+def time_steps(fn, steps: int, warmup: int, kernel: int):
+    """(ms per step over exactly `steps` calls, mean fused-kernel ms)."""
+    import torch
+    from chenxing_amd import _lib
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(steps):
+        fn()
+    b.record()
+    torch.cuda.synchronize()
+    step_ms = a.elapsed_time(b) / steps
+    # a second pass with the library's per-launch events for the kernel itself
+    _lib.timing_read(kernel)
+    _lib.timing_enable(True)
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    _lib.timing_enable(False)
+    kms, n = _lib.timing_read(kernel)
+    for k in range(5):
+        _lib.timing_read(k)
+    return step_ms, kms / max(n, 1)
+
+
+def cpu_baseline(w, seconds: float) -> dict:
+    """The oracle (``oracle.sampler_ref.sample_row``, numpy, one core) on as many
+    rows of the workload as fit in about `seconds`."""
+    from oracle import sampler_ref as R
+    hl = R.hist_rows_to_lists(w.hist, w.hist_len) if w.hist.size else None
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        b = n % w.B
+        R.sample_row(w.logits[b], w.params[b], None if hl is None else hl[b], float(w.u[b]))
+        n += 1
+        if time.perf_counter() - t0 >= seconds and n >= 8:
+            break
+    dt = time.perf_counter() - t0
+    return {"value": round(n / dt, 2), "unit": "rows/s", "cores": 1, "kind": "port",
+            "sample": f"{n} rows of the B={w.B} V={w.V} workload ({dt:.1f} s, numpy "
+                      f"{np.__version__}, single thread, {_cpu_model()})"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=500)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--quick", action="store_true", help="headline workload only")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU: the sampled rows are independent, so N GPUs "
+              "would each run their own B/N slice with no exchange; run with --gpus 1",
+              file=sys.stderr)
+        return 2
+
+    import torch
+    from chenxing_amd import _lib, workloads as W
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    _lib.load()
+    dev = torch.device("cuda:0")
+
+    _say("[bench] generating full_penalty workload")
+    w = W.full_penalty()
+    ds = DeviceSample(w, dev)
+    _say("[bench] timing full_penalty")
+    step_ms, kern_ms = time_steps(ds, args.steps, args.warmup, _lib.KERNEL_SAMPLE)
+    st = ds.st.cpu().numpy()
+    nbytes = W.algorithmic_bytes(w)
+    rows_per_s = w.B / (step_ms / 1e3)
+    achieved = nbytes / (kern_ms / 1e3) / 1e9
+    outcomes = {"ok": int(np.sum((st & 0xFF) == _lib.ROW_OK)),
+                "slow_path": int(np.sum((st & 0x100) != 0)),
+                "other": int(np.sum((st & 0xFF) != _lib.ROW_OK))}
+
+    other = {}
+    if not args.quick:
+        specs = [("nucleus", lambda: W.nucleus(), _lib.KERNEL_SAMPLE),
+                 ("nucleus_greedy", lambda: W.nucleus(greedy=True), _lib.KERNEL_SAMPLE),
+                 ("hetero_bf16", lambda: W.hetero_bf16(), _lib.KERNEL_SAMPLE),
+                 ("spec_verify", lambda: W.spec_verify(), _lib.KERNEL_VERIFY_STATS),
+                 ("spec_verify_greedy", lambda: W.spec_verify(greedy=True),
+                  _lib.KERNEL_VERIFY_STATS)]
+        for name, make, kernel in specs:
+            _say(f"[bench] {name}")
+            wk = make()
+            if name.startswith("spec"):
+                fn = DeviceVerify(wk, dev)
+                nb = W.verify_algorithmic_bytes(wk)
+                rows = wk.target.shape[0]
+            else:
+                fn = DeviceSample(wk, dev)
+                nb = W.algorithmic_bytes(wk)
+                rows = wk.B
+            steps = max(20, args.steps // 5)
+            sm, km = time_steps(fn, steps, max(5, args.warmup // 5), kernel)
+            entry = {"rows_per_s": round(rows / (sm / 1e3), 1), "ms_per_step": round(sm, 5),
+                     "algorithmic_bytes": nb, "step_GBps": round(nb / (sm / 1e3) / 1e9, 1),
+                     "main_kernel_ms": round(km, 5)}
+            if not name.startswith("spec"):
+                entry["slow_path_rows"] = int(np.sum((fn.st.cpu().numpy() & 0x100) != 0))
+            other[name] = entry
+            del fn
+            torch.cuda.empty_cache()
+
+    cpu = None
+    if args.cpu_seconds > 0:
+        _say("[bench] CPU baseline (oracle)")
+        cpu = cpu_baseline(w, args.cpu_seconds)
+
+    out = {
+        "metric": METRIC,
+        "value": round(rows_per_s, 1),
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "full_penalty", "B": w.B, "V": w.V, "history": 2048,
+                   "temperature": 0.7, "top_k": 40, "top_p": 0.9, "repetition_penalty": 1.1,
+                   "presence_penalty": 0.5, "frequency_penalty": 0.3, "parallelism": "none"},
+        "hbm_GBps": round(nbytes / (step_ms / 1e3) / 1e9, 1),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                     "traffic": None, "kernel": "cx::sample_kernel<false>",
+                     "kernel_ms": round(kern_ms, 5), "algorithmic_bytes": nbytes},
+        "cpu_baseline": cpu,
+        "row_outcomes": outcomes,
+        "other_workloads": other,
+    }
+    prof = os.path.join(HERE, "profiles", "sample_kernel_full_penalty_traffic.json")
+    if os.path.exists(prof):
+        with open(prof) as f:
+            out["roofline"]["traffic"] = json.load(f).get("traffic_bytes_per_launch")
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

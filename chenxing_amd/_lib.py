@@ -38,6 +38,8 @@ _SIGS = {
     "cx_spec_verify_workspace_bytes": (C.c_size_t, [C.c_int32, C.c_int32, C.c_int32]),
     "cx_spec_verify_host": (C.c_int, [_P, _P, _P, _P, _P, C.c_int32, C.c_int32, C.c_int32, _P,
                                       _P, _P, _P]),
+    "cx_timing_enable": (C.c_int, [C.c_int]),
+    "cx_timing_read": (C.c_int, [C.c_int32, _P, _P]),
     "cx_last_error": (C.c_char_p, []),
     "cx_version": (C.c_char_p, []),
 }
@@ -57,6 +59,13 @@ def load(path: str | None = None):
         if not os.path.exists(p):
             raise CxError(f"{p} is not built; run `python -m chenxing_amd.build` "
                           "(the sampler has no CPU fallback)")
+        # One HIP runtime per process: torch bundles its own libamdhip64.so.7,
+        # and the first copy loaded serves every later library with that
+        # soname, so torch (when installed) is loaded first.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         lib = C.CDLL(p)
         for name, (res, args) in _SIGS.items():
             fn = getattr(lib, name)
@@ -219,3 +228,19 @@ def header_symbols() -> list[str]:
     text = open(path).read()
     return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(cx_\w+)\s*\(", text,
                                  flags=re.M)))
+
+
+KERNEL_SAMPLE, KERNEL_SAMPLE_SLOW, KERNEL_VERIFY_STATS, KERNEL_VERIFY_REST, KERNEL_SAMPLE_FINISH = 0, 1, 2, 3, 4
+
+
+def timing_enable(on: bool = True) -> None:
+    load().cx_timing_enable(1 if on else 0)
+
+
+def timing_read(kernel: int) -> tuple[float, int]:
+    """(summed milliseconds, launches) of one kernel since the last read."""
+    lib = load()
+    ms = C.c_double()
+    n = C.c_int64()
+    _check(lib.cx_timing_read(kernel, C.cast(C.byref(ms), _P), C.cast(C.byref(n), _P)))
+    return ms.value, n.value

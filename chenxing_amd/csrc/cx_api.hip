@@ -8,6 +8,7 @@
 
 #include "cx_sampler.h"
 #include "cx_internal.hpp"
+#include "cx_timing.hpp"
 
 namespace cx {
 int launch_sample(const SampleArgs& A, hipStream_t s);
@@ -15,6 +16,11 @@ int launch_slow(const SampleArgs& A, hipStream_t s);
 int launch_verify(const VerifyArgs& A, bool any_stochastic, hipStream_t s);
 
 static thread_local std::string g_err;
+
+Timing& timing() {
+  static Timing t;
+  return t;
+}
 
 static int fail(int code, const char* fmt, ...) {
   char buf[512];
@@ -81,29 +87,35 @@ static int sample_impl(const void* logits, int bf16, int64_t ld, int32_t B, int3
   int per = (V + A.nsplit - 1) / A.nsplit;
   A.split_len = (per + 7) / 8 * 8;
   A.bf16 = bf16;
+  A.logV = log((double)V);
   const int esz = bf16 ? 2 : 4;
   A.vec_ok = (((uintptr_t)logits) % 16 == 0) && ((ld * esz) % 16 == 0);
+  const long win = ldh > 0 ? (ldh < WIN_MAX ? ldh : WIN_MAX) : 0;   // window capacity
   if (ldh > 0) {
-    long win = ldh < WIN_MAX ? ldh : WIN_MAX;
     A.ns = pow2_at_least(2 * win > 64 ? 2 * win : 64);
     A.ns_log2 = ilog2(A.ns);
-    long bits = pow2_at_least(A.split_len);
-    if (bits > (1 << 18)) bits = 1 << 18;
-    A.nbw = (int)(bits / 32 > 1 ? bits / 32 : 1);
   }
+  // fused kernel: penalty index (bitmap of the slice's window ids, hash of
+  // (id << 12 | count) words and the ids' raw logits) and the per-wave
+  // candidate buffers
+  const long nbw = ldh > 0 ? (A.split_len + 31) / 32 : 0;
+  const long nslot = ldh > 0 ? A.ns : 0;
   size_t off = 0;
   A.off_bitmap = 0;
-  off = align_up((size_t)A.nbw * 4, 16);
-  A.off_hkey = (int)off;
-  off += (size_t)A.ns * 4;
+  off = align_up((size_t)nbw * 4, 16);
+  A.off_hword = (int)off;
+  off += (size_t)nslot * 4;
   A.off_hval = (int)off;
-  off = align_up(off + (size_t)A.ns * 4, 16);
+  off = align_up(off + (size_t)nslot * 4, 16);
   A.off_wkey = (int)off;
   off += (size_t)16 * CAPW * 4;
   A.off_widx = (int)off;
   off += (size_t)16 * CAPW * 4;
-  size_t fin = (size_t)SORT_CAP * (8 + 4 + 4 + 8 + 8);
-  A.lds_bytes = (int)(off > fin ? off : fin);
+  A.off_gather = (int)off;
+  off += (size_t)LEAN_CAP * 12;
+  const size_t fin = (size_t)SORT_CAP * (8 + 4 + 4 + 8 + 8);
+  A.fin_lds_bytes = (int)fin;
+  A.lds_bytes = (int)(A.nsplit > 1 ? off : (off > fin ? off : fin));
   if (A.lds_bytes > 150 * 1024) return fail(CX_EINVAL, "LDS layout too large (%d)", A.lds_bytes);
   {  // multi-pass kernel: full-row bitmap + hash keys + histogram / gather work area
     long bits = ldh > 0 ? pow2_at_least(V) : 32;
@@ -294,6 +306,42 @@ int cx_spec_verify_host(const float* target, const float* draft, const int32_t* 
       (e = hipMemcpy(row_status, dst.p, (size_t)B * 4, hipMemcpyDeviceToHost)))
     return hip_fail(e, "hipMemcpy");
   return CX_OK;
+}
+
+int cx_timing_enable(int on) {
+  Timing& T = timing();
+  std::lock_guard<std::mutex> g(T.mu);
+  T.on = on != 0;
+  return CX_OK;
+}
+
+int cx_timing_read(int32_t kernel, double* total_ms, int64_t* launches) {
+  g_err.clear();
+  if (kernel < 0 || kernel > 4 || !total_ms || !launches) return fail(CX_EINVAL, "bad timing query");
+  Timing& T = timing();
+  std::vector<TimedLaunch> rec;
+  {
+    std::lock_guard<std::mutex> g(T.mu);
+    rec.swap(T.rec[kernel]);
+  }
+  double sum = 0.0;
+  int64_t n = 0;
+  int rc = CX_OK;
+  for (auto& r : rec) {
+    float ms = 0.f;
+    hipError_t e = hipEventSynchronize(r.b);
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, r.a, r.b);
+    if (e != hipSuccess) rc = hip_fail(e, "timing events");
+    sum += ms;
+    ++n;
+  }
+  {
+    std::lock_guard<std::mutex> g(T.mu);
+    for (auto& r : rec) { T.pool.push_back(r.a); T.pool.push_back(r.b); }
+  }
+  *total_ms = sum;
+  *launches = n;
+  return rc;
 }
 
 const char* cx_last_error(void) { return g_err.c_str(); }

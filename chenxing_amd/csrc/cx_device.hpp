@@ -13,6 +13,15 @@ namespace cx {
 constexpr int WG = 1024;
 constexpr int NWAVE = WG / 64;
 
+// LDS pointers: generic pointers that cross a call or a volatile access
+// become flat instructions (which also wait on outstanding global loads);
+// address space 3 keeps them ds_* operations.
+#define CX_LDS __attribute__((address_space(3)))
+template <typename T>
+__device__ __forceinline__ CX_LDS T* to_lds(T* p) { return (CX_LDS T*)p; }
+template <typename T>
+__device__ __forceinline__ T lds_load(const CX_LDS T* p) { return *(const volatile CX_LDS T*)p; }
+
 // ------------------------------------------------------------ orderable keys
 // Map a float to an unsigned integer whose unsigned order is the float order
 // (-inf < ... < -0 < +0 < ... < +inf).  0 is below every float and serves as
@@ -72,6 +81,76 @@ __device__ __forceinline__ void wave_argmax(double& v, int& i) {
     argmax_merge(v, i, w, j);
   }
 }
+
+// ------------------------------------------------------------ DPP reductions
+// Rotations inside each 16-lane row: one VALU op per 32 bits, no LDS trip.
+template <int N> __device__ __forceinline__ uint32_t dpp_ror(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x120 + N, 0xF, 0xF, false);
+}
+template <int N> __device__ __forceinline__ int dpp_ror(int v) {
+  return __builtin_amdgcn_mov_dpp(v, 0x120 + N, 0xF, 0xF, false);
+}
+template <int N> __device__ __forceinline__ float dpp_ror(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x120 + N, 0xF, 0xF, false));
+}
+template <int N> __device__ __forceinline__ double dpp_ror(double v) {
+  const uint64_t b = (uint64_t)__double_as_longlong(v);
+  const uint32_t lo = dpp_ror<N>((uint32_t)b), hi = dpp_ror<N>((uint32_t)(b >> 32));
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+__device__ __forceinline__ uint32_t lane_read(uint32_t v, int l) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, l);
+}
+__device__ __forceinline__ int lane_read(int v, int l) { return __builtin_amdgcn_readlane(v, l); }
+__device__ __forceinline__ float lane_read(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+__device__ __forceinline__ double lane_read(double v, int l) {
+  const uint64_t b = (uint64_t)__double_as_longlong(v);
+  const uint32_t lo = lane_read((uint32_t)b, l), hi = lane_read((uint32_t)(b >> 32), l);
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+// Every lane of a 16-lane row receives the row's reduction.
+template <typename T, typename Op>
+__device__ __forceinline__ T row_reduce(T v, Op op) {
+  v = op(v, dpp_ror<8>(v));
+  v = op(v, dpp_ror<4>(v));
+  v = op(v, dpp_ror<2>(v));
+  return op(v, dpp_ror<1>(v));
+}
+// The whole wave's reduction (uniform); row 0 only: lanes 0-15.
+template <typename T, typename Op>
+__device__ __forceinline__ T wave_reduce(T v, Op op) {
+  v = row_reduce(v, op);
+  return op(op(lane_read(v, 0), lane_read(v, 16)), op(lane_read(v, 32), lane_read(v, 48)));
+}
+template <typename T, typename Op>
+__device__ __forceinline__ T row0_reduce(T v, Op op) {
+  return lane_read(row_reduce(v, op), 0);
+}
+// Inclusive prefix sum across the 64 lanes with DPP row shifts and row
+// broadcasts (no LDS traffic).
+template <int CTRL, int ROWS>
+__device__ __forceinline__ double dpp_update0(double v) {
+  const uint64_t b = (uint64_t)__double_as_longlong(v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, CTRL, ROWS, 0xF, true);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), CTRL, ROWS, 0xF, true);
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+__device__ __forceinline__ double wave_scan_dpp(double v) {
+  v += dpp_update0<0x111, 0xF>(v);   // row_shr:1
+  v += dpp_update0<0x112, 0xF>(v);   // row_shr:2
+  v += dpp_update0<0x114, 0xF>(v);   // row_shr:4
+  v += dpp_update0<0x118, 0xF>(v);   // row_shr:8
+  v += dpp_update0<0x142, 0xA>(v);   // row_bcast:15 into rows 1 and 3
+  v += dpp_update0<0x143, 0xC>(v);   // row_bcast:31 into rows 2 and 3
+  return v;
+}
+
+struct OpAdd { template <typename T> __device__ T operator()(T a, T b) const { return a + b; } };
+struct OpMax { template <typename T> __device__ T operator()(T a, T b) const { return a > b ? a : b; } };
+struct OpMin { template <typename T> __device__ T operator()(T a, T b) const { return a < b ? a : b; } };
+struct OpOr { __device__ int operator()(int a, int b) const { return a | b; } };
 
 // Block-wide reductions through a small LDS scratch (>= NWAVE slots).
 template <typename T>
@@ -163,6 +242,54 @@ __device__ __forceinline__ Rec bitonic_pick(const Rec& r, const Rec& p, int e, i
   bool want_first = (lower == first_half_desc);
   bool r_first = rec_before(r, p);
   return (want_first == r_first) ? r : p;
+}
+
+// Sort up to 64 * PER records held by one wave in registers into
+// rec_before order.  Lane l holds elements l * PER .. l * PER + PER - 1;
+// strides below PER swap inside a lane, larger strides use shuffles.
+template <int S, int PER>
+__device__ __forceinline__ void lane_stage(Rec (&r)[PER], int l, int size) {
+  // compare-exchange of in-lane partners j and j ^ S (compile-time indices)
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    if ((j ^ S) > j) {
+      const int e = l * PER + j;
+      Rec lo = bitonic_pick(r[j], r[j ^ S], e, S, size);
+      Rec hi = bitonic_pick(r[j ^ S], r[j], e ^ S, S, size);
+      r[j] = lo;
+      r[j ^ S] = hi;
+    }
+  }
+}
+
+template <int PER>
+__device__ inline void wave_sort(Rec (&r)[PER]) {
+  static_assert(PER == 1 || PER == 2 || PER == 4, "PER");
+  const int l = lane_id();
+  constexpr int NP = 64 * PER;
+  for (int size = 2; size <= NP; size <<= 1) {
+    for (int stride = size >> 1; stride >= PER; stride >>= 1) {
+      const int ls = stride / PER;
+#pragma unroll
+      for (int j = 0; j < PER; ++j) {
+        Rec p = shfl_xor_rec(r[j], ls);
+        r[j] = bitonic_pick(r[j], p, l * PER + j, stride, size);
+      }
+    }
+    if constexpr (PER >= 4) {
+      if (size >= 4) lane_stage<2, PER>(r, l, size);
+    }
+    if constexpr (PER >= 2) lane_stage<1, PER>(r, l, size);
+  }
+}
+
+// Inclusive prefix sum across the 64 lanes of a wave.
+__device__ __forceinline__ double wave_incl_scan(double v) {
+  for (int o = 1; o < 64; o <<= 1) {
+    double w = __shfl_up(v, o);
+    if (lane_id() >= o) v += w;
+  }
+  return v;
 }
 
 // Sort n <= 2 * WG records held in LDS (k, i, a) into rec_before order.

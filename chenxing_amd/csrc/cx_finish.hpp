@@ -102,15 +102,17 @@ __device__ inline void finish_row(const SampleArgs& A, int row, const cx_row_par
   }
   double S = 0.0;
   uint32_t tau = 1u;
+  double tol = TOL_S;
   for (int s = 0; s < nsp; ++s) {
     if (st[s].s != 0.0) S += st[s].s * exp((st[s].m - M) * invT);
     tau = max(tau, st[s].tau);
+    tol = st[s].tol > tol ? st[s].tol : tol;
   }
   auto pending = [&]() { write_row_result(A, row, ROW_PENDING, -1); };
   // Degenerate rows (NaN / +inf / all -inf), tie floods, typical-p and a
   // possible P**(1/T) underflow (ln V / T > 740) go to the multi-pass kernel.
-  if (mnan || !(S > 0.0) || !(S < __builtin_inf()) || (flags & SF_OVERFLOW) ||
-      P.typical_p < 1.0 || log((double)A.V) * invT > 740.0) {
+  if (mnan || !(S > 0.0) || !(S < __builtin_inf()) || (flags & (SF_OVERFLOW | SF_INEXACT)) ||
+      P.typical_p < 1.0 || A.logV * invT > 740.0) {
     pending();
     return;
   }
@@ -199,7 +201,6 @@ __device__ inline void finish_row(const SampleArgs& A, int row, const cx_row_par
       if (sc[j] >= P.top_p) atomicMin(&f_j, j);
     __syncthreads();
     const int m = f_j;
-    const double tol = TOL_S;
     bool near;
     if (m < nk) {
       near = fabs(sc[m] - P.top_p) <= tol * sc[m] ||

@@ -11,12 +11,16 @@ constexpr int KW_MAX = 128;               // entries a wave keeps when it compac
 constexpr int SORT_CAP = 2048;            // finisher sort capacity (2 per thread)
 constexpr int WIN_MAX = 4095;             // longest penalty window held in LDS
 constexpr int CAPS = 16 * CAPW + 4096;    // candidates per (row, slice) in the workspace
+constexpr int LEAN_CAP = 256;             // region size the one-wave finisher sorts
 constexpr uint32_t HEMPTY = 0xFFFFFFFFu;  // empty hash slot
 constexpr double TOL_S = 4e-6;            // relative error bound of the fp32-term normaliser
+constexpr double TOL_T = 2e-6;            // relative error bound of one fp32 stream term
+constexpr double TOL_MAX = 1e-4;          // rows whose bound exceeds this are recomputed exactly
 
 // SplitStats.flags
 constexpr int SF_OVERFLOW = 1;            // a wave buffer flooded with ties
 constexpr int SF_UNSUPPORTED = 2;         // window longer than WIN_MAX
+constexpr int SF_INEXACT = 4;             // the slice's normaliser has no usable error bound
 
 // Internal row_status value: the finisher could not decide the row and the
 // multi-pass kernel must finish it.  Never returned to the caller.
@@ -26,7 +30,7 @@ struct SplitStats {       // one per (row, slice), 64 bytes
   double m;               // max of the slice's penalised values (stochastic rows)
   double s;               // sum of exp((x - m) / T) over the slice
   double best_v;          // first maximum (greedy rows)
-  double pad0;
+  double tol;             // relative error bound of s (stochastic rows)
   int32_t best_i;         // its index (INT_MAX if none)
   int32_t nan_i;          // first NaN index (INT_MAX if none)
   uint32_t tau;           // region threshold key; <= 1 means the region is the whole slice
@@ -58,12 +62,13 @@ struct SampleArgs {
   SplitStats* stats;      // [B * nsplit]
   Cand* cands;            // [B * nsplit * CAPS]
   int32_t nsplit, split_len;
-  int32_t ns, ns_log2;    // hash slots (power of two) and log2
-  int32_t nbw;            // bitmap words (power of two)
+  int32_t ns, ns_log2;    // penalty hash slots (power of two, >= 2 x window) and log2
   int32_t vec_ok;         // rows are 16-byte aligned
-  int32_t off_bitmap, off_hkey, off_hval, off_wkey, off_widx;
-  int32_t lds_bytes;
+  int32_t off_bitmap, off_hword, off_hval, off_wkey, off_widx, off_gather;
+  int32_t lds_bytes;      // fused kernel dynamic LDS
+  int32_t fin_lds_bytes;  // finish kernel dynamic LDS (several slices per row)
   int32_t bf16;
+  double logV;            // log(V)
   int32_t slow_nbw;       // multi-pass kernel: full-row bitmap words (power of two)
   int32_t slow_off_hkey, slow_off_work, slow_lds_bytes;
 };
@@ -112,11 +117,18 @@ struct SampleWorkspace {
 
 inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
+constexpr int SLICE_MAX = 1 << 18;        // elements per slice (bitmap index limit)
+
+// Slices per row: one when the batch alone fills the 256 CUs (no cross-
+// workgroup merge at all); otherwise enough slices for about 512 workgroups,
+// each at least 16384 elements long.
 inline int choose_nsplit(int B, int V) {
-  int by_rows = B >= 512 ? 1 : 512 / (B > 0 ? B : 1);
+  int n = B >= 256 ? 1 : (512 + B - 1) / (B > 0 ? B : 1);
   int by_len = V / 16384 > 0 ? V / 16384 : 1;
-  int n = by_rows < by_len ? by_rows : by_len;
+  if (n > by_len) n = by_len;
   if (n > 8) n = 8;
+  int need = (V + SLICE_MAX - 1) / SLICE_MAX;
+  if (n < need) n = need;
   return n < 1 ? 1 : n;
 }
 

@@ -2,78 +2,80 @@
 //
 // One launch samples a whole batch.  The grid is B x nsplit workgroups of
 // 1024 threads; workgroup (row, s) streams the contiguous slice s of row
-// `row` exactly once from HBM with 16-byte nontemporal loads and produces:
+// `row` exactly once from HBM.  The slice is cut into chunks of 64 x U
+// 16-byte vectors; each wave streams chunks with nontemporal buffer loads,
+// two chunks in flight, taking its next chunk from an LDS counter so the
+// waves of a workgroup finish together.  It produces:
 //
-//   * the penalised maximum and the temperature-scaled normaliser of its
-//     slice (online max / sum-exp, fp32 exp2 terms accumulated in fp64),
-//     or, for greedy rows, the first argmax;
-//   * an exact "region": every element of the slice whose value is >= a
-//     threshold tau, collected in per-wave LDS buffers.  Each wave keeps its
-//     own threshold, raised by a wave-local radix select whenever its
-//     buffer fills, so the hot loop has no workgroup barriers;
-//   * the penalised values of its history ids.  Penalties touch only ids in
-//     the history window, so the loop tests a bitmap in LDS (one ds_read per
-//     16-byte vector) and parks flagged elements; they are re-scored in fp64
-//     afterwards from an LDS hash table of (id, count).
+//   * stochastic rows: the sum of exp2(x * c - R), c = log2(e) / T, over the
+//     RAW logits (one fma + one v_exp_f32 per element, fp64 accumulation
+//     against a per-lane integer exponent R), and an exact "region": every
+//     unpenalised element at or above a threshold, appended to per-wave LDS
+//     buffers.  The waves publish their largest lane values in rank-sorted
+//     LDS slots and raise a shared threshold to the k-th largest published
+//     value, so after the first chunk only a few elements per wave still
+//     qualify.  Penalties touch only the history window's ids: their raw
+//     logits are gathered at the start, and afterwards each one's raw term
+//     is replaced by its penalised term in fp64 -- the hot loop never looks
+//     at penalties, except to keep penalised elements out of the region (a
+//     bitmap bit, tested only for elements above the threshold);
+//   * greedy rows: the first argmax over the unpenalised elements (a bitmap
+//     test per vector), merged with the penalised values afterwards.
 //
-// The last workgroup of a row to finish (agent-scope counter) runs
-// finish_row (cx_finish.hpp).  Rows it cannot decide are marked pending and
-// finished by the multi-pass kernel in cx_slow.hip.
+// Rows with one slice finish in the same workgroup: top-k rows with a small
+// region are decided by one wave; other rows write their region and
+// statistics and run finish_row (cx_finish.hpp), in the same workgroup or,
+// for several slices, in finish_kernel.  Rows none of these can decide are
+// marked pending and finished by the multi-pass kernel in cx_slow.hip.
 #include "cx_device.hpp"
 #include "cx_sampler.h"
 #include "cx_internal.hpp"
 #include "cx_finish.hpp"
+#include "cx_timing.hpp"
 
 namespace cx {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+#define CX_RELAXED_WG __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP
+
 // ------------------------------------------------------------ penalties
-__device__ __forceinline__ uint32_t hash_slot(int id, int ns_log2) {
-  return ((uint32_t)id * 0x9E3779B1u) >> (32 - ns_log2);
+// Penalty index of a slice [lo, hi): a bitmap of the window's ids (the
+// stream's test) and an open-addressing hash of the distinct ids, one word
+// (id << 12 | count in the window) and the id's raw logit per slot.  Ids are
+// below 2^20 and counts below 2^12, so no word equals HW_EMPTY.
+struct PenIndex {
+  CX_LDS uint32_t* bitmap;
+  CX_LDS uint32_t* hword;
+  CX_LDS float* hval;
+  int nbw;
+  int ns, ns_log2;
+};
+constexpr uint32_t HW_EMPTY = 0xFFFFFFFFu;
+constexpr int NSLOT = 4;                        // published lane keys per wave
+constexpr int HPT = (WIN_MAX + WG - 1) / WG;   // window entries per thread
+
+__device__ __forceinline__ bool pen_bit(const PenIndex& X, int r) {
+  return (X.bitmap[r >> 5] >> (r & 31)) & 1u;
 }
 
-// Insert one window id into the LDS table of (id << 12 | count) words.
-__device__ __forceinline__ void hash_insert(uint32_t* hkey, int ns_log2, int id) {
-  const uint32_t mask = (1u << ns_log2) - 1;
-  uint32_t s = hash_slot(id, ns_log2);
-  for (;;) {
-    uint32_t old = atomicCAS(&hkey[s], HEMPTY, ((uint32_t)id << 12) | 1u);
-    if (old == HEMPTY) return;
-    if ((old >> 12) == (uint32_t)id) { atomicAdd(&hkey[s], 1u); return; }
-    s = (s + 1) & mask;
-  }
-}
-
-__device__ __forceinline__ int hash_find(const uint32_t* hkey, int ns_log2, int id) {
-  const uint32_t mask = (1u << ns_log2) - 1;
-  uint32_t s = hash_slot(id, ns_log2);
-  for (;;) {
-    uint32_t k = hkey[s];
-    if (k == HEMPTY) return -1;
-    if ((k >> 12) == (uint32_t)id) return (int)s;
-    s = (s + 1) & mask;
-  }
-}
-
-// Bitmap + hash table for the window ids that fall in [lo, hi)
-// (sampler.py:67-68: window of the last max(64, n_keep) ids, out-of-range ids dropped).
-__device__ inline void build_penalty_tables(const int32_t* hrow, int wstart, int wlen, int lo,
-                                            int hi, uint32_t* bitmap, int nbw, uint32_t* hkey,
-                                            int ns, int ns_log2) {
-  for (int i = threadIdx.x; i < nbw; i += WG) bitmap[i] = 0u;
-  for (int i = threadIdx.x; i < ns; i += WG) hkey[i] = HEMPTY;
-  __syncthreads();
-  for (int i = threadIdx.x; i < wlen; i += WG) {
-    int id = hrow[wstart + i];
-    if (id >= lo && id < hi) {
-      int r = id - lo;
-      atomicOr(&bitmap[(r >> 5) & (nbw - 1)], 1u << (r & 31));
-      hash_insert(hkey, ns_log2, id);
+// Count one more occurrence of id; returns its slot, and in `created`
+// whether this call inserted it (one caller per distinct id).  Linear
+// probing; the table holds at least twice as many slots as window entries.
+__device__ __forceinline__ int pen_insert(const PenIndex& X, int id, bool& created) {
+  uint32_t h = ((uint32_t)id * 0x9E3779B1u) >> (32 - X.ns_log2);
+  const uint32_t w0 = (uint32_t)id << 12;
+  while (true) {
+    uint32_t prev = HW_EMPTY;
+    created = __hip_atomic_compare_exchange_strong(X.hword + h, &prev, w0, __ATOMIC_RELAXED,
+                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (created || (prev >> 12) == (uint32_t)id) {
+      __hip_atomic_fetch_add(X.hword + h, 1u, CX_RELAXED_WG);
+      return (int)h;
     }
+    h = (h + 1) & (uint32_t)(X.ns - 1);
   }
-  __syncthreads();
 }
 
 // fp64 penalised value of a history id: sampler.py:70-72, then the
@@ -91,6 +93,7 @@ __device__ __forceinline__ double penalise(float raw, int cnt, const cx_row_para
 template <bool BF16> struct Elem;
 template <> struct Elem<false> {
   static constexpr int NE = 4;
+  static constexpr int U = 4;      // vectors per lane per chunk
   using V = f32x4;
   __device__ static __forceinline__ void unpack(const V& q, float (&x)[NE]) {
     x[0] = q.x; x[1] = q.y; x[2] = q.z; x[3] = q.w;
@@ -101,6 +104,7 @@ template <> struct Elem<false> {
 };
 template <> struct Elem<true> {
   static constexpr int NE = 8;
+  static constexpr int U = 2;
   using V = u32x4;
   __device__ static __forceinline__ void unpack(const V& q, float (&x)[NE]) {
     const uint32_t w[4] = {q.x, q.y, q.z, q.w};
@@ -115,21 +119,84 @@ template <> struct Elem<true> {
   }
 };
 
+// Buffer descriptor over `bytes` bytes at p: loads past the end return 0, so
+// the stream needs no clamped addresses.  Word 3 is the raw-buffer format of
+// gfx9 parts.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const void* p, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, bytes, 0x00020000);
+}
+// 16-byte nontemporal load at byte offset voff + soff (soff wave-uniform).
+template <bool BF16>
+__device__ __forceinline__ typename Elem<BF16>::V bload(__amdgpu_buffer_rsrc_t rs, int voff,
+                                                       int soff) {
+  return __builtin_bit_cast(typename Elem<BF16>::V,
+                            __builtin_amdgcn_raw_buffer_load_b128(rs, voff, soff, 2));
+}
+// The U vectors of this lane in chunk ch: vectors ch * 64U + u * 64 + lane.
+template <bool BF16>
+__device__ __forceinline__ void load_chunk(__amdgpu_buffer_rsrc_t rs, int ch,
+                                           typename Elem<BF16>::V (&q)[Elem<BF16>::U]) {
+  constexpr int U = Elem<BF16>::U;
+#pragma unroll
+  for (int u = 0; u < U; ++u) q[u] = bload<BF16>(rs, lane_id() * 16, (ch * 64 * U + u * 64) * 16);
+}
+// Next chunk for this wave from the workgroup's counter.
+__device__ __forceinline__ int next_chunk(CX_LDS int* counter) {
+  int v = 0;
+  if (lane_id() == 0) v = __hip_atomic_fetch_add(counter, 1, CX_RELAXED_WG);
+  return __builtin_amdgcn_readfirstlane(v);
+}
+
+// The k-th largest of the 64 lane values (1 <= k <= 64): two key bits per
+// step, three independent ballot counts each.
+__device__ __noinline__ uint32_t kth_of_lanes(uint32_t v, int k) {
+  uint32_t prefix = 0u;
+  for (int sh = 30; sh >= 0; sh -= 2) {
+    const uint32_t b1 = prefix | (1u << sh), b2 = prefix | (2u << sh), b3 = prefix | (3u << sh);
+    const int c3 = __popcll(ballot(v >= b3));
+    const int c2 = __popcll(ballot(v >= b2));
+    const int c1 = __popcll(ballot(v >= b1));
+    prefix = c3 >= k ? b3 : (c2 >= k ? b2 : (c1 >= k ? b1 : prefix));
+  }
+  return prefix;
+}
+
 // ------------------------------------------------------------ wave candidates
-// Wave-uniform state: every lane holds the same n / tau / overflow, and every
-// update is made by all 64 lanes from ballots.
+// Wave-uniform state: every lane holds the same n / tau / overflow.  tau only
+// rises.  `cnt` is the LDS copy of n that lanes bump when they append on
+// their own.  `shared` is the slice's shared threshold word: the highest
+// proven lower bound of the slice's k-th largest unpenalised value.
 struct WaveBuf {
-  uint32_t* key;
-  int32_t* idx;
+  CX_LDS uint32_t* key;
+  CX_LDS int32_t* idx;
+  CX_LDS int* cnt;
+  CX_LDS uint32_t* shared;
   int n;
-  uint32_t tau;   // every element seen so far with key >= tau is in the buffer
+  uint32_t tau;   // every unpenalised element seen with key >= tau is held
+  float tauf;     // tau as a float; -inf while tau <= 1 (everything)
   int kw;         // entries a compaction keeps
   bool overflow;
 };
 
+__device__ __forceinline__ void raise_tau(WaveBuf& w, uint32_t t) {
+  if (t > w.tau) {
+    w.tau = t;
+    w.tauf = key2f(t);
+  }
+}
+
+// State travels by value so nothing of the caller lives in memory.
+struct WState {
+  int n;
+  uint32_t tau;
+};
+
 // Raise tau to the kw-th largest key held (bitwise radix select over the
-// buffer with ballot counts) and drop the entries below it.
-__device__ __noinline__ void wave_compact(WaveBuf& w) {
+// buffer with ballot counts) and drop the entries below it.  Not inlined: it
+// is the cold path of the stream.
+__device__ __noinline__ WState wave_compact_call(CX_LDS uint32_t* wkey, CX_LDS int32_t* widx,
+                                                 int n, uint32_t tau, int kw, bool share,
+                                                 CX_LDS uint32_t* shared) {
   constexpr int PER = CAPW / 64;
   const int l = lane_id();
   uint32_t k[PER];
@@ -137,123 +204,501 @@ __device__ __noinline__ void wave_compact(WaveBuf& w) {
 #pragma unroll
   for (int e = 0; e < PER; ++e) {
     int pos = l + 64 * e;
-    k[e] = pos < w.n ? w.key[pos] : 0u;
-    id[e] = pos < w.n ? w.idx[pos] : 0;
+    k[e] = pos < n ? wkey[pos] : 0u;
+    id[e] = pos < n ? widx[pos] : 0;
   }
-  uint32_t prefix = 0;
-  for (int bit = 31; bit >= 0; --bit) {
+  // bits every held key shares need no radix step
+  uint32_t kand = 0xFFFFFFFFu, kor = 0u;
+#pragma unroll
+  for (int e = 0; e < PER; ++e)
+    if (k[e]) { kand &= k[e]; kor |= k[e]; }
+  for (int o = 32; o > 0; o >>= 1) {
+    kand &= __shfl_xor(kand, o);
+    kor |= __shfl_xor(kor, o);
+  }
+  const uint32_t diff = kand ^ kor;
+  const int hb = diff ? 31 - __clz(diff) : -1;
+  uint32_t prefix = hb < 0 ? kand : (hb == 31 ? 0u : (kand & ~((2u << hb) - 1u)));
+  for (int bit = hb; bit >= 0; --bit) {
     uint32_t cand = prefix | (1u << bit);
     int cnt = 0;
 #pragma unroll
     for (int e = 0; e < PER; ++e) cnt += __popcll(ballot(k[e] >= cand));
-    if (cnt >= w.kw) prefix = cand;
+    if (cnt >= kw) prefix = cand;
   }
-  if (prefix > w.tau) w.tau = prefix;
-  int n = 0;
+  if (prefix > tau) tau = prefix;
+  int m = 0;
 #pragma unroll
   for (int e = 0; e < PER; ++e) {
-    bool keep = k[e] >= w.tau && k[e] != 0u;
+    bool keep = k[e] >= tau && k[e] != 0u;
     uint64_t b = ballot(keep);
     if (keep) {
-      int p = n + lanes_below(b);
-      w.key[p] = k[e];
-      w.idx[p] = id[e];
+      int p = m + lanes_below(b);
+      wkey[p] = k[e];
+      widx[p] = id[e];
     }
-    n += __popcll(b);
+    m += __popcll(b);
   }
-  w.n = n;
+  // a wave's kw-th largest bounds the slice's k-th largest when kw == k
+  if (share && l == 0) __hip_atomic_fetch_max(shared, tau, CX_RELAXED_WG);
+  WState r;
+  r.n = m;
+  r.tau = tau;
+  return r;
 }
+
+__device__ __forceinline__ void wave_compact(WaveBuf& w, bool share) {
+  WState r = wave_compact_call(w.key, w.idx, w.n, w.tau, w.kw, share, w.shared);
+  w.n = r.n;
+  raise_tau(w, r.tau);
+}
+
+// Insert one element slot of the wave (key 0 = not a candidate), compacting
+// when the buffer is full.  Returns whether this lane's key went in.
+__device__ __forceinline__ bool wave_insert1(WaveBuf& w, uint32_t key, int idx, bool share) {
+  bool p = key >= w.tau;
+  uint64_t b = ballot(p);
+  if (b == 0) return false;
+  int c = __popcll(b);
+  if (w.n + c > CAPW) {
+    wave_compact(w, share);
+    p = key >= w.tau;
+    b = ballot(p);
+    c = __popcll(b);
+    if (w.n + c > CAPW) { w.overflow = true; return false; }
+  }
+  if (p) {
+    int pos = w.n + lanes_below(b);
+    w.key[pos] = key;
+    w.idx[pos] = idx;
+  }
+  w.n += c;
+  return p;
+}
+
+// ------------------------------------------------------------ shared thresholds
+// Every lane keeps ck, the key of the largest unpenalised element it has
+// seen at or above its wave's threshold (or in its first chunk): distinct
+// lanes hold distinct elements, and ck only grows.
+//
+// Slot scheme (top-k rows, k <= 64): wave w writes its m = NSLOT largest
+// lane keys, rank-sorted, to slots[m w .. m w + m).  Slot j of a wave
+// is the (j+1)-th largest lane key, which only grows; a reader that catches
+// a wave mid-update therefore never counts more slots >= v than the wave has
+// distinct elements >= v, and the k-th largest of the 64 slots is a lower
+// bound of the slice's k-th largest unpenalised value.
+__device__ __forceinline__ void publish_top(uint32_t ck, int m, CX_LDS uint32_t* slots) {
+  uint32_t v = ck;
+  for (int j = 0; j < m; ++j) {
+    const uint32_t M = wave_reduce(v, OpMax());
+    if (lane_id() == 0) slots[j] = M;
+    const uint64_t b = ballot(v == M);
+    if (lane_id() == __builtin_ctzll(b)) v = 0u;
+  }
+}
+// Minimum scheme (64 < k <= 64 * NWAVE): each wave publishes its r-th largest
+// lane key; NWAVE * r distinct elements reach the minimum over the waves.
+__device__ __forceinline__ uint32_t pub_min(const CX_LDS uint32_t* w_pub) {
+  uint32_t m = lane_id() < NWAVE ? lds_load(w_pub + lane_id()) : 0xFFFFFFFFu;
+  for (int o = 32; o > 0; o >>= 1) {
+    const uint32_t v = (uint32_t)__shfl_xor((int)m, o);
+    m = v < m ? v : m;
+  }
+  return m;
+}
+// Publish this wave's values and raise the shared threshold with them.
+__device__ __forceinline__ void publish(uint32_t ck, int krow, int pub_r, CX_LDS uint32_t* slots,
+                                        CX_LDS uint32_t* w_pub, CX_LDS uint32_t* shared) {
+  uint32_t T = 0u;
+  if (krow <= 64) {
+    publish_top(ck, NSLOT, slots + NSLOT * wave_id());
+    T = kth_of_lanes(lds_load(slots + lane_id()), krow);
+  } else if (pub_r > 0) {
+    const uint32_t th = kth_of_lanes(ck, pub_r);
+    if (lane_id() == 0 && th > w_pub[wave_id()]) w_pub[wave_id()] = th;
+    T = pub_min(w_pub);
+  }
+  if (lane_id() == 0 && T > 1u) __hip_atomic_fetch_max(shared, T, CX_RELAXED_WG);
+}
+
+// ------------------------------------------------------------ stochastic stream
+// The sum is taken against a per-lane integer exponent R: terms
+// exp2(x * c - R) stay finite while x <= top = (value that set R) + 32 / c,
+// so R moves only on such a jump, and the fp64 sum is then rescaled by an
+// exact power of two.  The fp32 argument of a term is within half an ulp of
+// 64 of the exact one, so a term is within TOL_T of its exact value.
+struct SState {
+  float R;      // integer-valued exponent offset (-inf before the first value)
+  float top;
+  double s;
+};
 
 template <int NE>
-__device__ __forceinline__ void wave_insert(WaveBuf& w, const uint32_t (&key)[NE], int64_t e0) {
+__device__ __forceinline__ void sum_terms(const float (&x)[NE], float vmax, float c, float lim,
+                                          SState& st) {
+  if (vmax > st.top) {
+    // vmax * c may overflow to +inf: R = +inf, the row's sum turns NaN or 0
+    // and the row goes to the multi-pass kernel
+    const float Rn = __builtin_ceilf(vmax * c);
+    if (st.s != 0.0) st.s = __builtin_ldexp(st.s, (int)fmaxf(st.R - Rn, -2048.0f));
+    st.R = Rn;
+    st.top = vmax + lim;
+  }
+  const float nR = fminf(-st.R, 3.402823466e38f);   // finite while R is -inf
+  float ts = __builtin_amdgcn_exp2f(__builtin_fmaf(x[0], c, nR));
 #pragma unroll
-  for (int j = 0; j < NE; ++j) {
-    bool p = key[j] >= w.tau;
-    uint64_t b = ballot(p);
-    if (b == 0) continue;
-    int c = __popcll(b);
-    if (w.n + c > CAPW) {
-      wave_compact(w);
-      p = key[j] >= w.tau;
-      b = ballot(p);
-      c = __popcll(b);
-      if (w.n + c > CAPW) { w.overflow = true; continue; }
+  for (int j = 1; j < NE; ++j) ts += __builtin_amdgcn_exp2f(__builtin_fmaf(x[j], c, nR));
+  st.s += (double)ts;
+}
+
+// Append the candidates of one chunk (some lane of the wave has one; bit u
+// of cm: vector u of this lane reaches the threshold).  With room for every
+// element of every flagged vector, lanes append on their own through the LDS
+// counter; otherwise the element slots go through wave_insert1 one by one.
+// Penalised elements never enter: their penalised values join afterwards.
+template <bool BF16>
+__device__ __forceinline__ void append_chunk(WaveBuf& wb, const typename Elem<BF16>::V (&q)[Elem<BF16>::U],
+                                             uint32_t cm, int vb, int nv, int lo, bool pen_on,
+                                             const PenIndex& X, bool share, uint32_t& ck) {
+  using E = Elem<BF16>;
+  constexpr int NE = E::NE;
+  constexpr int U = E::U;
+  int bound = 0;
+#pragma unroll
+  for (int u = 0; u < U; ++u) bound += __popcll(ballot((cm >> u) & 1u));
+  if (wb.n + bound * NE <= CAPW) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (!ballot((cm >> u) & 1u)) continue;
+      if ((cm >> u) & 1u) {
+        float x[NE];
+        E::unpack(q[u], x);
+        const int e0 = (vb + u * 64) * NE + lo;
+#pragma unroll
+        for (int j = 0; j < NE; ++j) {
+          if (x[j] >= wb.tauf && !(pen_on && pen_bit(X, e0 + j - lo))) {
+            const uint32_t k = f2key(x[j]);
+            const int pos = __hip_atomic_fetch_add(wb.cnt, 1, CX_RELAXED_WG);
+            wb.key[pos] = k;
+            wb.idx[pos] = e0 + j;
+            ck = k > ck ? k : ck;
+          }
+        }
+      }
     }
-    if (p) {
-      int pos = w.n + lanes_below(b);
-      w.key[pos] = key[j];
-      w.idx[pos] = (int32_t)(e0 + j);
+    wb.n = lds_load(wb.cnt);
+  } else {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float x[NE];
+      E::unpack(q[u], x);
+      const int vi = vb + u * 64;
+      const bool valid = vi < nv;
+      const int e0 = vi * NE + lo;
+#pragma unroll
+      for (int j = 0; j < NE; ++j) {
+        uint32_t k = 0u;
+        if (valid && x[j] >= wb.tauf && !(pen_on && pen_bit(X, e0 + j - lo))) k = f2key(x[j]);
+        if (wave_insert1(wb, k, e0 + j, share)) ck = k > ck ? k : ck;
+      }
     }
-    w.n += c;
+    if (lane_id() == 0) *wb.cnt = wb.n;
   }
 }
 
-// ------------------------------------------------------------ per-thread stream state
-struct StochState {
-  float m;     // running max of unparked values
-  double s;    // sum of exp2((x - m) * c), c = log2(e) / T
-};
+// Stream the vectors of a stochastic slice.  Vector i covers elements
+// lo + i*NE .. lo + i*NE + NE-1, i < nv; q holds this wave's first chunk
+// (chunk wave_id()), loaded by the caller.
+template <bool BF16>
+__device__ __forceinline__ void stream_stoch(__amdgpu_buffer_rsrc_t rs,
+                                             typename Elem<BF16>::V (&q)[Elem<BF16>::U], int nv,
+                                             int lo, bool pen_on, const PenIndex& X, float c,
+                                             int krow, int pub_r, CX_LDS int* chunk_ctr,
+                                             CX_LDS uint32_t* slots, CX_LDS uint32_t* w_pub,
+                                             SState& st, WaveBuf& wb, uint32_t& ck) {
+  using E = Elem<BF16>;
+  constexpr int NE = E::NE;
+  constexpr int U = E::U;
+  constexpr int CH = 64 * U;
+  const float lim = 32.0f / c;
+  const bool share = true;
+  const int nch = (nv + CH - 1) / CH;
+  const int nfull = nv / CH;
+  int ch = wave_id();
+  int cn = ch < nch ? next_chunk(chunk_ctr) : nch;
+  bool fresh = false;              // appended since the last publication
+  for (int it = 0; ch < nch; ++it) {
+    typename E::V qn[U];
+    if (cn < nch) load_chunk<BF16>(rs, cn, qn);
+    const int cnn = cn < nch ? next_chunk(chunk_ctr) : nch;
+    raise_tau(wb, lds_load(wb.shared));
+    const int vb = ch * CH + lane_id();
+    uint32_t cm = 0u;
+    if (ch < nfull) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        float x[NE];
+        E::unpack(q[u], x);
+        float vmax = x[0];
+#pragma unroll
+        for (int j = 1; j < NE; ++j) vmax = fmaxf(vmax, x[j]);
+        sum_terms<NE>(x, vmax, c, lim, st);
+        cm |= (vmax >= wb.tauf ? 1u : 0u) << u;
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const bool valid = vb + u * 64 < nv;
+        float x[NE];
+        E::unpack(q[u], x);
+#pragma unroll
+        for (int j = 0; j < NE; ++j) x[j] = valid ? x[j] : -__builtin_inff();
+        float vmax = x[0];
+#pragma unroll
+        for (int j = 1; j < NE; ++j) vmax = fmaxf(vmax, x[j]);
+        sum_terms<NE>(x, vmax, c, lim, st);
+        cm |= (valid && vmax >= wb.tauf ? 1u : 0u) << u;
+      }
+    }
+    if (ballot(cm != 0u)) {
+      append_chunk<BF16>(wb, q, cm, vb, nv, lo, pen_on, X, share, ck);
+      fresh = true;
+    }
+    if ((it == 1 || it == 3) && fresh) {
+      publish(ck, krow, pub_r, slots, w_pub, wb.shared);
+      raise_tau(wb, lds_load(wb.shared));
+      fresh = false;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) q[u] = qn[u];
+    ch = cn;
+    cn = cnn;
+  }
+}
+
+// Scalar elements [s0, hi) of a stochastic slice (unaligned rows, or the
+// tail after the last whole vector).
+template <bool BF16>
+__device__ __forceinline__ void stream_scalar(const char* rowp, int s0, int lo, int hi,
+                                              bool pen_on, const PenIndex& X, float c, bool share,
+                                              SState& st, WaveBuf& wb, uint32_t& ck) {
+  using E = Elem<BF16>;
+  const float lim = 32.0f / c;
+  for (int e = s0 + lane_id() + 64 * wave_id(); e - lane_id() < hi; e += WG) {
+    const bool valid = e < hi;
+    float x1[1] = {valid ? E::scalar(rowp, e) : -__builtin_inff()};
+    sum_terms<1>(x1, x1[0], c, lim, st);
+    uint32_t k = 0u;
+    if (valid && x1[0] >= wb.tauf && !(pen_on && pen_bit(X, e - lo))) k = f2key(x1[0]);
+    if (ballot(k != 0u)) {
+      wb.n = lds_load(wb.cnt);
+      if (wave_insert1(wb, k, e, share)) ck = k > ck ? k : ck;
+      if (lane_id() == 0) *wb.cnt = wb.n;
+    }
+  }
+}
+
+// ------------------------------------------------------------ greedy stream
 struct GreedyState {
   float bv;
   int bi;
   int nan_i;
 };
 
-// One 16-byte vector (or one scalar, NE == 1).  Called by all 64 lanes of
-// the wave; `valid` is false for lanes past the end of the slice.
-template <int NE, bool GREEDY>
-__device__ __forceinline__ void process_vec(const float (&xin)[NE], int64_t e0, bool valid,
-                                            int lo, bool has_pen, const uint32_t* bitmap,
-                                            int nbw, const uint32_t* hkey, float* hval,
-                                            int ns_log2, float c, StochState& st,
-                                            GreedyState& gs, WaveBuf& wb) {
-  uint32_t parked = valid ? 0u : 0xFFu;
-  if (has_pen && valid) {
-    int r = (int)(e0 - lo);
-    uint32_t word = bitmap[(r >> 5) & (nbw - 1)];
-    uint32_t bits = (word >> (r & 31)) & ((1u << NE) - 1u);
-    if (bits) {
-#pragma unroll
-      for (int j = 0; j < NE; ++j)
-        if (bits & (1u << j)) {
-          int sl = hash_find(hkey, ns_log2, (int)(e0 + j));
-          if (sl >= 0) { hval[sl] = xin[j]; parked |= 1u << j; }
-        }
-    }
+// One vector (or scalar, NE == 1): first argmax over the unpenalised,
+// valid elements (penalised ones are merged with their penalised values
+// afterwards).
+template <int NE>
+__device__ __forceinline__ void greedy_vec(const float (&x)[NE], int e0, bool valid, int lo,
+                                           bool has_pen, const PenIndex& X, GreedyState& gs) {
+  if (!valid) return;
+  uint32_t bits = 0u;
+  if (has_pen) {
+    const int r = e0 - lo;
+    bits = (X.bitmap[r >> 5] >> (r & 31)) & ((1u << NE) - 1u);
   }
-  if (GREEDY) {
-#pragma unroll
-    for (int j = 0; j < NE; ++j) {
-      if (parked & (1u << j)) continue;
-      float x = xin[j];
-      if (x > gs.bv) { gs.bv = x; gs.bi = (int)(e0 + j); }
-      if (x != x && gs.nan_i == INT_MAX) gs.nan_i = (int)(e0 + j);
-    }
-    return;
-  }
-  float x[NE];
-  float vmax = -__builtin_inff();
 #pragma unroll
   for (int j = 0; j < NE; ++j) {
-    x[j] = (parked & (1u << j)) ? -__builtin_inff() : xin[j];
-    vmax = fmaxf(vmax, x[j]);
+    if (bits & (1u << j)) continue;
+    if (x[j] > gs.bv) { gs.bv = x[j]; gs.bi = e0 + j; }
+    if (x[j] != x[j] && gs.nan_i == INT_MAX) gs.nan_i = e0 + j;
   }
-  if (vmax > st.m) {
-    if (st.s != 0.0) st.s *= exp2((double)(st.m - vmax) * (double)c);
-    st.m = vmax;
-  }
-  const float mm = fmaxf(st.m, -3.402823466e38f);
-  float tsum = 0.f;
-  uint32_t key[NE];
-  uint32_t kmax = 0;
+}
+
+template <bool BF16>
+__device__ __forceinline__ void stream_greedy(const char* rowp, __amdgpu_buffer_rsrc_t rs,
+                                              typename Elem<BF16>::V (&q)[Elem<BF16>::U], int nv,
+                                              int lo, int hi, int s0, bool pen_on,
+                                              const PenIndex& X, CX_LDS int* chunk_ctr,
+                                              GreedyState& gs) {
+  using E = Elem<BF16>;
+  constexpr int NE = E::NE;
+  constexpr int U = E::U;
+  constexpr int CH = 64 * U;
+  const int nch = (nv + CH - 1) / CH;
+  int ch = wave_id();
+  int cn = ch < nch ? next_chunk(chunk_ctr) : nch;
+  while (ch < nch) {
+    typename E::V qn[U];
+    if (cn < nch) load_chunk<BF16>(rs, cn, qn);
+    const int cnn = cn < nch ? next_chunk(chunk_ctr) : nch;
+    const int vb = ch * CH + lane_id();
 #pragma unroll
-  for (int j = 0; j < NE; ++j) {
-    tsum += __builtin_amdgcn_exp2f((x[j] - mm) * c);
-    key[j] = (parked & (1u << j)) ? 0u : f2key(x[j]);
-    kmax = key[j] > kmax ? key[j] : kmax;
+    for (int u = 0; u < U; ++u) {
+      float x[NE];
+      E::unpack(q[u], x);
+      const int vi = vb + u * 64;
+      greedy_vec<NE>(x, vi * NE + lo, vi < nv, lo, pen_on, X, gs);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) q[u] = qn[u];
+    ch = cn;
+    cn = cnn;
   }
-  st.s += (double)tsum;
-  if (ballot(kmax >= wb.tau)) wave_insert<NE>(wb, key, e0);
+  for (int e = s0 + threadIdx.x; e < hi; e += WG) {
+    float x1[1] = {E::scalar(rowp, e)};
+    greedy_vec<1>(x1, e, true, lo, pen_on, X, gs);
+  }
+}
+
+// ------------------------------------------------------------ one-wave finish
+struct LeanLds {          // one wave's work area (72 slots: unrolled reads overrun)
+  uint64_t k[72];         // kept keys, list order
+  int32_t i[72];
+  uint64_t sk[72];        // rank order
+  int32_t si[72];
+  double q[72];
+};
+
+// Wave 0 decides a top-k row (k <= 64) from the region list: the entries at
+// or above thr64 (at most 64, else the cut is raised to the k-th largest)
+// are ranked (value descending, id ascending) by counting, cut by top-k
+// (ties kept), top-p and min-p, and one is drawn in token-id order.
+// Returns false when the row needs the exact path (near a top-p boundary,
+// fewer than k records above a proper threshold, or more than 64 records
+// tied into the top-k).
+__device__ inline bool lean_decide(const SampleArgs& A, int row, const cx_row_params& P,
+                                   const CX_LDS uint64_t* gk, const CX_LDS int32_t* gi, int nlist,
+                                   uint64_t thr64, double kc, double Rb, double S, double tol,
+                                   CX_LDS LeanLds* L, double u, int& tok) {
+  const int l = lane_id();
+  constexpr int PER = LEAN_CAP / 64;
+  uint64_t k[PER];
+  int32_t id[PER];
+  int E = 0;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int e = l + 64 * j;
+    k[j] = e < nlist ? gk[e] : 0ull;
+    id[j] = e < nlist ? gi[e] : INT_MAX;
+    if (k[j] < thr64) k[j] = 0ull;
+    E += __popcll(ballot(k[j] != 0ull));
+  }
+  if (E < P.top_k && thr64 > 1ull) return false;
+  uint64_t cut = 1ull;
+  if (E > 64) {
+    // raise the cut to the k-th largest kept key, two bits per step
+    uint64_t prefix = 0ull;
+    for (int sh = 62; sh >= 0; sh -= 2) {
+      const uint64_t b1 = prefix | (1ull << sh), b2 = prefix | (2ull << sh),
+                     b3 = prefix | (3ull << sh);
+      int c1 = 0, c2 = 0, c3 = 0;
+#pragma unroll
+      for (int j = 0; j < PER; ++j) {
+        c3 += __popcll(ballot(k[j] >= b3));
+        c2 += __popcll(ballot(k[j] >= b2));
+        c1 += __popcll(ballot(k[j] >= b1));
+      }
+      prefix = c3 >= P.top_k ? b3 : (c2 >= P.top_k ? b2 : (c1 >= P.top_k ? b1 : prefix));
+    }
+    cut = prefix;
+  }
+  int base = 0;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const bool keep = k[j] != 0ull && k[j] >= cut;
+    const uint64_t b = ballot(keep);
+    const int pos = base + lanes_below(b);
+    if (keep && pos < 64) { L->k[pos] = k[j]; L->i[pos] = id[j]; }
+    base += __popcll(b);
+  }
+  E = base;
+  if (E > 64) return false;
+  // sentinels past the kept entries (key 0 is below every value, id above
+  // every id), so the unrolled scans below need no bounds tests
+  if (l < 8) { L->k[E + l] = 0ull; L->i[E + l] = INT_MAX; }
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  // (1) rank = number of kept entries before this one; 8 entries per step
+  const uint64_t mk = l < E ? L->k[l] : 0ull;
+  const int32_t mi = l < E ? L->i[l] : INT_MAX;
+  int rank = 0;
+  for (int i = 0; i < E; i += 8) {
+    uint64_t ki[8];
+    int32_t ii[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) { ki[j] = L->k[i + j]; ii[j] = L->i[i + j]; }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) rank += (ki[j] > mk || (ki[j] == mk && ii[j] < mi)) ? 1 : 0;
+  }
+  if (l < E) { L->sk[rank] = mk; L->si[rank] = mi; }
+  if (l < 8) L->si[E + l] = INT_MAX;
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  const uint64_t key = l < E ? L->sk[l] : 0ull;
+  const int32_t idx = l < E ? L->si[l] : INT_MAX;
+  // (2) top-k: every record at or above the k-th largest value
+  int n = E;
+  if (P.top_k < E) {
+    const uint64_t kth = L->sk[P.top_k - 1];
+    n = __popcll(ballot(l < E && key >= kth));
+  }
+  // (3) probabilities of the kept prefix; top-p on the unrenormalised vector
+  const double Pj = l < n ? exp2(key2d(key) * kc - Rb) / S : 0.0;
+  if (P.top_p < 1.0) {                                 // sampler.py:81-89
+    const double cum = wave_scan_dpp(Pj);
+    const uint64_t b = ballot(l < n && cum >= P.top_p);
+    bool near;
+    if (b) {
+      const int mm = __builtin_ctzll(b);
+      const double cm = lane_read(cum, mm);
+      const double cp = lane_read(cum, mm > 0 ? mm - 1 : 0);
+      near = fabs(cm - P.top_p) <= tol * cm || (mm > 0 && fabs(cp - P.top_p) <= tol * cp);
+      n = mm + 1;
+    } else {
+      const double cl = lane_read(cum, n - 1);
+      near = fabs(cl - P.top_p) <= tol * cl;
+    }
+    if (near) return false;                            // exact fp64 normaliser needed
+  }
+  if (P.min_p > 0.0) {                                 // sampler.py:91-93
+    const double floor_p = P.min_p * lane_read(Pj, 0);
+    const uint64_t b = ballot(l < n && Pj < floor_p);
+    if (b) n = __builtin_ctzll(b);
+  }
+  // (4) normalise and draw in token-id order (sampler.py:123-127; choice ==
+  // searchsorted(cumsum / last, u, 'right')): F = mass of the kept records
+  // with an id <= this one
+  const double qv = l < n ? Pj : 0.0;
+  const double Z = wave_reduce(qv, OpAdd());
+  const double qi = qv / Z;
+  L->q[l] = qi;                                        // 0 past the kept prefix
+  if (l < 8) L->q[64 + l] = 0.0;
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  double F = 0.0;
+  for (int i = 0; i < n; i += 8) {
+    int32_t ii[8];
+    double qq[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) { ii[j] = L->si[i + j]; qq[j] = L->q[i + j]; }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) F += ii[j] <= idx ? qq[j] : 0.0;
+  }
+  const double last = wave_reduce(l < n ? F : 0.0, OpMax());
+  const int pick = wave_reduce((l < n && F / last > u) ? idx : INT_MAX, OpMin());
+  tok = pick != INT_MAX ? pick : wave_reduce(l < n ? idx : -1, OpMax());
+  return true;
 }
 
 // ------------------------------------------------------------ the kernel
@@ -261,23 +706,33 @@ template <bool BF16>
 __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   using E = Elem<BF16>;
   constexpr int NE = E::NE;
+  constexpr int U = E::U;
+  constexpr int CH = 64 * U;
   extern __shared__ __align__(16) unsigned char dyn[];
   __shared__ double red_d[2 * NWAVE + 4];
   __shared__ int red_i[2 * NWAVE + 4];
-  __shared__ uint32_t w_tau[NWAVE];
-  __shared__ int w_n[NWAVE];
-  __shared__ int w_ovf[NWAVE];
+  __shared__ double w_s[NWAVE], w_pr[NWAVE], w_corr[NWAVE], w_pmx[NWAVE], w_Rc[NWAVE];
+  __shared__ float w_R[NWAVE];
+  __shared__ uint32_t w_tau[NWAVE], w_kmx[NWAVE];
+  __shared__ int w_fl[NWAVE];
+  __shared__ int w_cnt[NWAVE];
+  __shared__ uint32_t s_shared;
+  __shared__ uint32_t w_pub[NWAVE];
+  __shared__ uint32_t slots[4 * NWAVE];
+  __shared__ int s_chunk;
   __shared__ int s_cnt;
-  __shared__ int s_last;
+  __shared__ LeanLds s_lean;
 
   const int row = blockIdx.x / A.nsplit;
   const int split = blockIdx.x % A.nsplit;
   const int t = threadIdx.x;
   const cx_row_params P = A.prm[row];
+  const double u_row = A.u[row];
   const bool greedy = P.temperature == 0.0;
   const int lo = split * A.split_len;
   const int hi = min(A.V, lo + A.split_len);
   const char* rowp = (const char*)A.logits + (size_t)row * (size_t)A.ld * (BF16 ? 2 : 4);
+  const bool single = A.nsplit == 1;
 
   int wlen = 0, wstart = 0;
   if (A.ldh > 0) {
@@ -290,194 +745,337 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   SplitStats* my = A.stats + (size_t)row * A.nsplit + split;
   Cand* mycand = A.cands + ((size_t)row * A.nsplit + split) * CAPS;
 
-  if (pen_on && wlen > WIN_MAX) {                    // window longer than the LDS table
+  if (pen_on && wlen > WIN_MAX) {                    // window longer than the LDS index
     if (t == 0) {
       my->flags = SF_UNSUPPORTED; my->ncand = 0; my->tau = 1u;
-      my->m = 0; my->s = 0; my->best_i = INT_MAX; my->nan_i = INT_MAX;
+      my->m = 0; my->s = 0; my->tol = 0; my->best_i = INT_MAX; my->nan_i = INT_MAX;
     }
-  } else {
-    uint32_t* bitmap = (uint32_t*)(dyn + A.off_bitmap);
-    uint32_t* hkey = (uint32_t*)(dyn + A.off_hkey);
-    float* hval = (float*)(dyn + A.off_hval);
-    if (pen_on)
-      build_penalty_tables(A.hist + (size_t)row * A.ldh, wstart, wlen, lo, hi, bitmap, A.nbw,
-                           hkey, A.ns, A.ns_log2);
-
-    WaveBuf wb;
-    wb.key = (uint32_t*)(dyn + A.off_wkey) + wave_id() * CAPW;
-    wb.idx = (int32_t*)(dyn + A.off_widx) + wave_id() * CAPW;
-    wb.n = 0;
-    wb.tau = 1u;
-    wb.overflow = false;
-    // Entries a wave keeps: k for top-k rows; otherwise an equal share of the
-    // finisher's sort capacity, so the merged region fits in LDS.
-    const int share = max(8, min(KW_MAX, SORT_CAP / (NWAVE * A.nsplit)));
-    wb.kw = P.top_k > 0 ? min(P.top_k, KW_MAX) : share;
-
-    const float c = (float)(1.4426950408889634 / (greedy ? 1.0 : P.temperature));
-    StochState st{-__builtin_inff(), 0.0};
-    GreedyState gs{-__builtin_inff(), INT_MAX, INT_MAX};
-
-    // ---- the slice: aligned 16-byte vectors, then a scalar tail
-    const int64_t v0 = A.vec_ok ? lo / NE : 0;
-    const int64_t v1 = A.vec_ok ? hi / NE : 0;
-    const typename E::V* vp = (const typename E::V*)rowp;
-    constexpr int U = BF16 ? 2 : 4;
-    for (int64_t base = v0 + t; base - t < v1; base += (int64_t)U * WG) {
-      typename E::V q[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        int64_t vi = base + (int64_t)u * WG;
-        if (vi < v1) q[u] = __builtin_nontemporal_load(&vp[vi]);
-      }
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        int64_t vi = base + (int64_t)u * WG;
-        if (vi - t >= v1) break;                       // uniform: no lane of the wave left
-        bool valid = vi < v1;
-        float x[NE];
-        if (valid) E::unpack(q[u], x);
-        else
-#pragma unroll
-          for (int j = 0; j < NE; ++j) x[j] = -__builtin_inff();
-        if (greedy)
-          process_vec<NE, true>(x, vi * NE, valid, lo, pen_on, bitmap, A.nbw, hkey, hval,
-                                A.ns_log2, c, st, gs, wb);
-        else
-          process_vec<NE, false>(x, vi * NE, valid, lo, pen_on, bitmap, A.nbw, hkey, hval,
-                                 A.ns_log2, c, st, gs, wb);
-      }
-    }
-    {   // scalar elements: [lo, hi) for unaligned rows, else the tail past v1*NE
-      const int64_t s0 = A.vec_ok ? (v1 * NE > lo ? v1 * NE : lo) : lo;
-      for (int64_t e = s0 + t; e - t < hi; e += WG) {
-        bool valid = e < hi;
-        float x1[1] = {valid ? E::scalar(rowp, e) : -__builtin_inff()};
-        if (greedy)
-          process_vec<1, true>(x1, e, valid, lo, pen_on, bitmap, A.nbw, hkey, hval, A.ns_log2,
-                               c, st, gs, wb);
-        else
-          process_vec<1, false>(x1, e, valid, lo, pen_on, bitmap, A.nbw, hkey, hval, A.ns_log2,
-                                c, st, gs, wb);
-      }
-    }
-
-    // Final compaction: each buffer becomes exactly its wave's top-kw (+ ties).
-    if (!greedy && wb.n > wb.kw) wave_compact(wb);
-
-    // ---- slice statistics
-    if (lane_id() == 0) {
-      w_tau[wave_id()] = wb.tau;
-      w_n[wave_id()] = wb.n;
-      w_ovf[wave_id()] = wb.overflow ? 1 : 0;
-    }
-    if (t == 0) s_cnt = 0;
+    if (!single) return;
     __syncthreads();
-    uint32_t tau_s = 1u;
-    int ovf = 0;
-    for (int w = 0; w < NWAVE; ++w) { tau_s = max(tau_s, w_tau[w]); ovf |= w_ovf[w]; }
-
-    if (greedy) {
-      double bv = gs.bi == INT_MAX ? -__builtin_inf() : (double)gs.bv;
-      int bi = gs.bi;
-      int ni = gs.nan_i;
-      if (pen_on)
-        for (int sl = t; sl < A.ns; sl += WG) {
-          uint32_t k = hkey[sl];
-          if (k == HEMPTY) continue;
-          int id = (int)(k >> 12);
-          double xp = penalise(hval[sl], (int)(k & 0xFFFu), P);
-          if (xp != xp) ni = min(ni, id);
-          else argmax_merge(bv, bi, xp, id);
-        }
-      block_argmax(bv, bi, red_d, red_i);
-      ni = block_min(ni, red_i, INT_MAX);
-      if (t == 0) {
-        my->m = 0; my->s = 0; my->best_v = bv; my->best_i = bi; my->nan_i = ni;
-        my->tau = 1u; my->ncand = 0; my->flags = 0;
-      }
-    } else {
-      const double invT = 1.0 / P.temperature;
-      float Mu = block_max(st.m, (float*)red_d, -__builtin_inff());
-      double su = 0.0;
-      if (st.s != 0.0) su = st.s * exp2((double)(st.m - Mu) * (double)c);
-      double Su = block_sum(su, red_d);
-      double mp = -__builtin_inf();
-      int pnan = 0;
-      if (pen_on)
-        for (int sl = t; sl < A.ns; sl += WG) {
-          uint32_t k = hkey[sl];
-          if (k == HEMPTY) continue;
-          double xp = penalise(hval[sl], (int)(k & 0xFFFu), P);
-          if (xp != xp) pnan = 1;
-          else mp = xp > mp ? xp : mp;
-        }
-      double Ms = (double)Mu;
-      if (pen_on) {
-        double Mp = block_max(mp, red_d, -__builtin_inf());
-        Ms = Mp > Ms ? Mp : Ms;
-        if (block_max(pnan, red_i, 0)) Ms = __builtin_nan("");
-      }
-      double Ss = Su == 0.0 ? 0.0 : Su * exp(((double)Mu - Ms) * invT);
-      const uint64_t thr64 = tau_s <= 1u ? 0ull : d2key((double)key2f(tau_s));
-      if (pen_on) {
-        double sp = 0.0;
-        for (int sl = t; sl < A.ns; sl += WG) {
-          uint32_t k = hkey[sl];
-          if (k == HEMPTY) continue;
-          int id = (int)(k >> 12);
-          double xp = penalise(hval[sl], (int)(k & 0xFFFu), P);
-          sp += exp((xp - Ms) * invT);
-          uint64_t k64 = d2key(xp);
-          if (k64 >= thr64 && xp == xp) {
-            int pos = atomicAdd(&s_cnt, 1);
-            mycand[pos].key = k64;
-            mycand[pos].idx = id;
-          }
-        }
-        Ss += block_sum(sp, red_d);
-      }
-      {   // region entries of this wave's buffer
-        const int w = wave_id();
-        const uint32_t* wk = (const uint32_t*)(dyn + A.off_wkey) + w * CAPW;
-        const int32_t* wi = (const int32_t*)(dyn + A.off_widx) + w * CAPW;
-        const int n = w_n[w];
-        for (int e = lane_id(); e - lane_id() < n; e += 64) {
-          bool keep = e < n && wk[e] >= tau_s;
-          uint64_t b = ballot(keep);
-          int base = 0;
-          if (lane_id() == 0 && b) base = atomicAdd(&s_cnt, (int)__popcll(b));
-          base = __shfl(base, 0);
-          if (keep) {
-            int pos = base + lanes_below(b);
-            mycand[pos].key = d2key((double)key2f(wk[e]));
-            mycand[pos].idx = wi[e];
-          }
-        }
-      }
-      __syncthreads();
-      if (t == 0) {
-        my->m = Ms; my->s = Ss; my->best_v = 0; my->best_i = INT_MAX; my->nan_i = INT_MAX;
-        my->tau = tau_s; my->ncand = s_cnt; my->flags = ovf ? SF_OVERFLOW : 0;
-      }
-    }
+    finish_row(A, row, P, dyn, red_d, red_i);
+    return;
   }
 
-  // ---- the last workgroup of the row finishes it
+  // the window ids first, then this wave's first chunk: both are in flight
+  // while the index tables are cleared
+  int32_t hid[HPT];
+#pragma unroll
+  for (int k = 0; k < HPT; ++k) {
+    const int i = t + k * WG;
+    hid[k] = (pen_on && i < wlen) ? A.hist[(size_t)row * A.ldh + wstart + i] : -1;
+  }
+  const int nv = A.vec_ok ? (hi - lo) / NE : 0;       // whole vectors of the slice
+  const int s0 = lo + nv * NE;                         // first scalar element
+  const __amdgpu_buffer_rsrc_t rs = row_rsrc(rowp + (size_t)lo * (BF16 ? 2 : 4), nv * 16);
+  typename E::V q[U];
+  if (wave_id() * CH < nv) load_chunk<BF16>(rs, wave_id(), q);
+
+  PenIndex X;
+  X.bitmap = to_lds((uint32_t*)(dyn + A.off_bitmap));
+  X.hword = to_lds((uint32_t*)(dyn + A.off_hword));
+  X.hval = to_lds((float*)(dyn + A.off_hval));
+  X.nbw = (hi - lo + 31) >> 5;
+  X.ns = pen_on ? A.ns : 0;
+  X.ns_log2 = A.ns_log2;
+  if (t == 0) { s_shared = 1u; s_chunk = NWAVE; s_cnt = 0; }
+  if (t < NWAVE) { w_pub[t] = 0u; w_cnt[t] = 0; }
+  if (t < 4 * NWAVE) slots[t] = 0u;
+  if (pen_on) {
+    for (int i = t; i < X.nbw; i += WG) X.bitmap[i] = 0u;
+    for (int i = t; i < X.ns; i += WG) X.hword[i] = HW_EMPTY;
+  }
   __syncthreads();
-  if (A.nsplit > 1) {
-    if (t == 0) {
-      __threadfence();
-      int old = __hip_atomic_fetch_add(&A.counters[row], 1, __ATOMIC_ACQ_REL,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-      s_last = (old == A.nsplit - 1) ? 1 : 0;
-      if (s_last)
-        __hip_atomic_store(&A.counters[row], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __threadfence();
+  // index the window ids of this slice; the thread that inserts a distinct
+  // id owns it and fetches its raw logit (not waited for until the end)
+  int hslot[HPT];
+  float gval[HPT];
+#pragma unroll
+  for (int k = 0; k < HPT; ++k) {
+    const int id = hid[k];
+    hslot[k] = -1;
+    if (id >= lo && id < hi) {
+      __hip_atomic_fetch_or(X.bitmap + ((id - lo) >> 5), 1u << ((id - lo) & 31), CX_RELAXED_WG);
+      bool created;
+      const int h = pen_insert(X, id, created);
+      if (created) hslot[k] = h;
     }
-    __syncthreads();
-    if (!s_last) return;
   }
+#pragma unroll
+  for (int k = 0; k < HPT; ++k) gval[k] = hslot[k] >= 0 ? E::scalar(rowp, hid[k]) : 0.0f;
+  __syncthreads();
+
+  // ---------------------------------------------------------------- greedy
+  if (greedy) {
+    GreedyState gs{-__builtin_inff(), INT_MAX, INT_MAX};
+    stream_greedy<BF16>(rowp, rs, q, nv, lo, hi, s0, pen_on, X, to_lds(&s_chunk), gs);
+    double bv = gs.bi == INT_MAX ? -__builtin_inf() : (double)gs.bv;
+    int bi = gs.bi;
+    int ni = gs.nan_i;
+#pragma unroll
+    for (int k = 0; k < HPT; ++k) {
+      if (hslot[k] < 0) continue;
+      const double xp = penalise(gval[k], (int)(X.hword[hslot[k]] & 0xFFFu), P);
+      if (xp != xp) ni = min(ni, hid[k]);
+      else argmax_merge(bv, bi, xp, hid[k]);
+    }
+    block_argmax(bv, bi, red_d, red_i);
+    ni = block_min(ni, red_i, INT_MAX);
+    if (single) {
+      const int tok = ni != INT_MAX ? ni : (bi == INT_MAX ? 0 : bi);
+      write_row_result(A, row, CX_ROW_GREEDY, tok);
+      write_one_hot(A, row, tok);
+    } else if (t == 0) {
+      my->m = 0; my->s = 0; my->tol = 0; my->best_v = bv; my->best_i = bi; my->nan_i = ni;
+      my->tau = 1u; my->ncand = 0; my->flags = 0;
+    }
+    return;
+  }
+
+  // ---------------------------------------------------------------- stochastic
+  const float c = (float)(1.4426950408889634 / P.temperature);
+  const double kc = (double)c;
+  WaveBuf wb;
+  wb.key = to_lds((uint32_t*)(dyn + A.off_wkey) + wave_id() * CAPW);
+  wb.idx = to_lds((int32_t*)(dyn + A.off_widx) + wave_id() * CAPW);
+  wb.cnt = to_lds(&w_cnt[wave_id()]);
+  wb.shared = to_lds(&s_shared);
+  wb.n = 0;
+  wb.tau = 1u;
+  wb.tauf = -__builtin_inff();
+  wb.overflow = false;
+  // Entries a wave keeps: k for top-k rows; otherwise an equal share of the
+  // finisher's sort capacity, so the merged region fits in LDS.
+  const int share = max(8, min(KW_MAX, SORT_CAP / (NWAVE * A.nsplit)));
+  wb.kw = P.top_k > 0 ? min(P.top_k, KW_MAX) : share;
+  // elements the shared threshold must leave: k of a top-k row, or 1024
+  // region entries of a top-p row
+  const int krow = P.top_k > 0 ? P.top_k : SORT_CAP / 2;
+  const int pub_r = krow > 64 && krow <= 64 * NWAVE ? (krow + NWAVE - 1) / NWAVE : 0;
+  CX_LDS uint32_t* const lslots = to_lds(slots);
+  CX_LDS uint32_t* const lpub = to_lds(w_pub);
+
+  // seed: every lane's largest unpenalised element of its first chunk
+  uint32_t ck = 0u;
+  if (wave_id() * CH < nv) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int vi = wave_id() * CH + u * 64 + lane_id();
+      float x[NE];
+      E::unpack(q[u], x);
+#pragma unroll
+      for (int j = 0; j < NE; ++j) {
+        const bool ok = vi < nv && x[j] == x[j] && !(pen_on && pen_bit(X, vi * NE + j));
+        const uint32_t k = ok ? f2key(x[j]) : 0u;
+        ck = k > ck ? k : ck;
+      }
+    }
+  }
+  if (krow <= 64) publish_top(ck, NSLOT, lslots + NSLOT * wave_id());
+  else if (pub_r > 0) {
+    const uint32_t th = kth_of_lanes(ck, pub_r);
+    if (lane_id() == 0) lpub[wave_id()] = th;
+  }
+  __syncthreads();
+  if (krow <= 64) raise_tau(wb, kth_of_lanes(lds_load(lslots + lane_id()), krow));
+  else if (pub_r > 0) raise_tau(wb, pub_min(lpub));
+
+  SState st{-__builtin_inff(), -__builtin_inff(), 0.0};
+  stream_stoch<BF16>(rs, q, nv, lo, pen_on, X, c, krow, pub_r, to_lds(&s_chunk), lslots, lpub,
+                     st, wb, ck);
+  if (s0 < hi) {
+    raise_tau(wb, lds_load(wb.shared));
+    stream_scalar<BF16>(rowp, s0, lo, hi, pen_on, X, c, true, st, wb, ck);
+  }
+
+  // ---- per wave, after its stream: (a) its region entries into the shared
+  // list, (b) the window ids its threads own -- raw terms out, penalised
+  // terms in, against the wave's own exponent offset Rc -- (c) its sums and
+  // state for the combination
+  uint64_t* gk = (uint64_t*)(dyn + A.off_gather);
+  int32_t* gi = (int32_t*)(dyn + A.off_gather + LEAN_CAP * 8);
+  CX_LDS uint64_t* const lgk = to_lds(gk);
+  CX_LDS int32_t* const lgi = to_lds(gi);
+  CX_LDS int* const lcnt = to_lds(&s_cnt);
+  raise_tau(wb, lds_load(wb.shared));
+  {
+    const int n = wb.n;
+    for (int e = lane_id(); e < n; e += 64) {
+      const uint32_t k = wb.key[e];
+      if (k >= wb.tau) {
+        const int pos = __hip_atomic_fetch_add(lcnt, 1, CX_RELAXED_WG);
+        if (pos < LEAN_CAP) { lgk[pos] = d2key((double)key2f(k)); lgi[pos] = wb.idx[e]; }
+      }
+    }
+  }
+  const float Rw = wave_reduce(st.R, OpMax());
+  double sl = st.s != 0.0 ? __builtin_ldexp(st.s, (int)fmaxf(st.R - Rw, -2048.0f)) : 0.0;
+  double corr = 0.0, pr = 0.0, pmx = -__builtin_inf();
+  int fl = st.s != st.s ? 1 : 0;
+  double Rc = -__builtin_inf();
+  {
+    double pm = -__builtin_inf();
+    double xpk[HPT];
+#pragma unroll
+    for (int k = 0; k < HPT; ++k) {
+      xpk[k] = 0.0;
+      if (hslot[k] < 0) continue;
+      X.hval[hslot[k]] = gval[k];                      // for the general path
+      xpk[k] = penalise(gval[k], (int)(X.hword[hslot[k]] & 0xFFFu), P);
+      const double xr = (double)gval[k];
+      pm = xr > pm ? xr : pm;
+      pm = xpk[k] > pm ? xpk[k] : pm;
+    }
+    pm = wave_reduce(pm, OpMax());
+    // every correction term is at most 1; NaN / +-inf windows leave Rc at 0
+    // (their rows are resolved by the multi-pass kernel)
+    Rc = (pm > -__builtin_inf() && pm < __builtin_inf()) ? ceil(pm * kc) : 0.0;
+    const double thr_w = wb.tau <= 1u ? -__builtin_inf() : (double)key2f(wb.tau);
+#pragma unroll
+    for (int k = 0; k < HPT; ++k) {
+      if (hslot[k] < 0) continue;
+      const double xp = xpk[k];
+      const double tr = exp2((double)gval[k] * kc - Rc);
+      const double tp = exp2(xp * kc - Rc);
+      pr += tr;
+      corr += tp - tr;
+      if (xp != xp) {
+        fl = 1;
+      } else {
+        pmx = xp > pmx ? xp : pmx;
+        if (xp >= thr_w) {
+          const int pos = __hip_atomic_fetch_add(lcnt, 1, CX_RELAXED_WG);
+          if (pos < LEAN_CAP) { lgk[pos] = d2key(xp); lgi[pos] = hid[k]; }
+        }
+      }
+    }
+  }
+  sl = wave_reduce(sl, OpAdd());
+  corr = wave_reduce(corr, OpAdd());
+  pr = wave_reduce(pr, OpAdd());
+  pmx = wave_reduce(pmx, OpMax());
+  const uint32_t kmx_w = wave_reduce(ck, OpMax());
+  fl = wave_reduce(fl, OpOr());
+  if (krow <= 64) publish_top(ck, NSLOT, lslots + NSLOT * wave_id());
+  if (lane_id() == 0) {
+    w_s[wave_id()] = sl;
+    w_corr[wave_id()] = corr;
+    w_pr[wave_id()] = pr;
+    w_pmx[wave_id()] = pmx;
+    w_Rc[wave_id()] = Rc;
+    w_R[wave_id()] = Rw;
+    w_tau[wave_id()] = wb.tau;
+    w_kmx[wave_id()] = kmx_w;
+    w_fl[wave_id()] = fl | (wb.overflow ? 2 : 0);
+  }
+  __syncthreads();
+
+  // ---- combine: S = sum over waves of 2^(Rw - Rb) s_w + 2^(Rc_w - Rb) corr_w
+  // (lane w of row 0 reads wave w's record)
+  const int lw = lane_id() & 15;
+  const float Rl = w_R[lw];
+  const double Rcl = w_Rc[lw];
+  const float Rf = row0_reduce(Rl, OpMax());
+  uint32_t Tf = row0_reduce(w_tau[lw], OpMax());
+  const uint32_t kmx = row0_reduce(w_kmx[lw], OpMax());
+  const int flw = row0_reduce(w_fl[lw], OpOr());
+  const int anynan = flw & 1, ovf = flw & 2;
+  if (krow <= 64) Tf = max(Tf, kth_of_lanes(lds_load(lslots + lane_id()), krow));
+  const double PMX = row0_reduce(w_pmx[lw], OpMax());
+  const double Rb = fmax((double)Rf, row0_reduce(Rcl, OpMax()));
+  // an exponent offset past +-2^22 leaves fp32 term arguments inexact
+  const bool rb_ok = Rf > -__builtin_inff() && fabs(Rb) < 4194304.0;
+  double Ss = 0.0, PR = 0.0;
+  if (rb_ok) {
+    const double sw = w_s[lw];
+    const double cw = w_corr[lw], pw = w_pr[lw];
+    const int dc = (int)fmax(Rcl - Rb, -2048.0);
+    const double term = (sw != 0.0 ? __builtin_ldexp(sw, (int)fmax((double)Rl - Rb, -2048.0)) : 0.0) +
+                        (cw != 0.0 ? __builtin_ldexp(cw, dc) : 0.0);
+    Ss = row0_reduce(term, OpAdd());
+    PR = row0_reduce(pw != 0.0 ? __builtin_ldexp(pw, dc) : 0.0, OpAdd());
+  }
+  const double invT = 1.0 / P.temperature;
+  const double tol = TOL_S + 2.0 * TOL_T * PR / Ss;
+  const bool sum_ok = !anynan && rb_ok && Ss > 0.0 && Ss < __builtin_inf() && tol <= TOL_MAX;
+  const int nlist = s_cnt;
+
+  // ---- lean finish (one slice, top-k <= 64, short list, nothing exotic)
+  if (single && sum_ok && !ovf && P.top_k > 0 && P.top_k <= 64 && P.typical_p >= 1.0 &&
+      !A.out_probs && A.logV * invT <= 740.0 && nlist <= LEAN_CAP) {
+    if (wave_id() != 0) return;
+    const uint64_t thr64 = Tf <= 1u ? 1ull : d2key((double)key2f(Tf));
+    int tok = -1;
+    const bool ok = lean_decide(A, row, P, lgk, lgi, nlist, thr64, kc, Rb, Ss, tol,
+                                to_lds(&s_lean), u_row, tok);
+    if (lane_id() == 0) {
+      A.out_id[row] = ok ? tok : -1;
+      A.row_status[row] = ok ? CX_ROW_OK : ROW_PENDING;
+    }
+    return;
+  }
+
+  // ---- general: bound the region, write it and the statistics, then finish
+  if (wb.n > wb.kw) {
+    wave_compact(wb, false);
+    if (lane_id() == 0) w_tau[wave_id()] = wb.tau;
+  }
+  if (t == 0) s_cnt = 0;
+  __syncthreads();
+  Tf = max(Tf, row0_reduce(w_tau[lw], OpMax()));
+  const uint64_t thr64 = Tf <= 1u ? 0ull : d2key((double)key2f(Tf));
+  for (int s = t; s < X.ns; s += WG) {
+    const uint32_t hw = X.hword[s];
+    if (hw == HW_EMPTY) continue;
+    const double xp = penalise(X.hval[s], (int)(hw & 0xFFFu), P);
+    const uint64_t k64 = d2key(xp);
+    if (k64 >= thr64 && xp == xp) {
+      const int pos = atomicAdd(&s_cnt, 1);
+      mycand[pos].key = k64;
+      mycand[pos].idx = (int32_t)(hw >> 12);
+    }
+  }
+  {
+    const int n = wb.n;
+    for (int e = lane_id(); e - lane_id() < n; e += 64) {
+      const bool keep = e < n && wb.key[e] >= Tf;
+      const uint64_t b = ballot(keep);
+      int base = 0;
+      if (lane_id() == 0 && b) base = atomicAdd(&s_cnt, (int)__popcll(b));
+      base = __shfl(base, 0);
+      if (keep) {
+        const int pos = base + lanes_below(b);
+        mycand[pos].key = d2key((double)key2f(wb.key[e]));
+        mycand[pos].idx = wb.idx[e];
+      }
+    }
+  }
+  __syncthreads();
+  if (t == 0) {
+    // the maximum of the slice's penalised values, and the sum against it
+    const double Mu = kmx ? (double)key2f(kmx) : -__builtin_inf();
+    const double Ms = Mu > PMX ? Mu : PMX;
+    my->m = Ms;
+    my->s = sum_ok ? Ss * exp2(Rb - Ms * kc) : Ss;
+    my->tol = tol;
+    my->best_v = 0; my->best_i = INT_MAX; my->nan_i = INT_MAX;
+    my->tau = Tf; my->ncand = s_cnt;
+    my->flags = (ovf ? SF_OVERFLOW : 0) | (sum_ok ? 0 : SF_INEXACT);
+  }
+  // one slice per row: this workgroup finishes the row.  Several slices:
+  // finish_kernel runs after the grid (a kernel boundary makes the slices'
+  // results visible across XCDs without per-workgroup cache writebacks).
+  if (!single) return;
+  __syncthreads();
+  finish_row(A, row, P, dyn, red_d, red_i);
+}
+
+// Finisher for rows computed in several slices: one workgroup per row.
+__global__ __launch_bounds__(WG) void finish_kernel(SampleArgs A) {
+  extern __shared__ __align__(16) unsigned char dyn[];
+  __shared__ double red_d[2 * NWAVE + 4];
+  __shared__ int red_i[2 * NWAVE + 4];
+  const int row = blockIdx.x;
+  const cx_row_params P = A.prm[row];
   finish_row(A, row, P, dyn, red_d, red_i);
 }
 
@@ -496,10 +1094,24 @@ int launch_sample(const SampleArgs& A, hipStream_t s) {
     if (e != hipSuccess) return (int)e;
     attr_set[A.bf16] = A.lds_bytes;
   }
-  if (A.bf16)
-    hipLaunchKernelGGL(sample_kernel<true>, dim3(A.B * A.nsplit), dim3(WG), A.lds_bytes, s, A);
-  else
-    hipLaunchKernelGGL(sample_kernel<false>, dim3(A.B * A.nsplit), dim3(WG), A.lds_bytes, s, A);
+  {
+    TimedScope ts(CX_KERNEL_SAMPLE, s);
+    if (A.bf16)
+      hipLaunchKernelGGL(sample_kernel<true>, dim3(A.B * A.nsplit), dim3(WG), A.lds_bytes, s, A);
+    else
+      hipLaunchKernelGGL(sample_kernel<false>, dim3(A.B * A.nsplit), dim3(WG), A.lds_bytes, s, A);
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || A.nsplit == 1) return (int)e;
+  static int fin_attr = 0;
+  if (A.fin_lds_bytes > fin_attr) {
+    e = hipFuncSetAttribute((const void*)finish_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            A.fin_lds_bytes);
+    if (e != hipSuccess) return (int)e;
+    fin_attr = A.fin_lds_bytes;
+  }
+  TimedScope tf(CX_KERNEL_SAMPLE_FINISH, s);
+  hipLaunchKernelGGL(finish_kernel, dim3(A.B), dim3(WG), A.fin_lds_bytes, s, A);
   return (int)hipGetLastError();
 }
 }  // namespace cx

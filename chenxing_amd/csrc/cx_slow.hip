@@ -19,6 +19,7 @@
 #include "cx_device.hpp"
 #include "cx_sampler.h"
 #include "cx_internal.hpp"
+#include "cx_timing.hpp"
 
 namespace cx {
 
@@ -518,6 +519,7 @@ int launch_slow(const SampleArgs& A, hipStream_t s) {
     if (e != hipSuccess) return (int)e;
     attr = A.slow_lds_bytes;
   }
+  TimedScope ts(CX_KERNEL_SAMPLE_SLOW, s);
   hipLaunchKernelGGL(slow_kernel, dim3(A.B), dim3(WG), A.slow_lds_bytes, s, A);
   return (int)hipGetLastError();
 }

@@ -22,6 +22,7 @@
 #include "cx_device.hpp"
 #include "cx_sampler.h"
 #include "cx_internal.hpp"
+#include "cx_timing.hpp"
 
 namespace cx {
 
@@ -409,7 +410,11 @@ __global__ __launch_bounds__(WG) void verify_draw(VerifyArgs A) {
 int launch_verify(const VerifyArgs& A, bool any_stochastic, hipStream_t s) {
   const int nt = A.B * (A.gamma + 1);
   const int nrows = nt + (any_stochastic ? A.B * A.gamma : 0);
-  hipLaunchKernelGGL(verify_stats, dim3(nrows * A.nchunk), dim3(WG), 0, s, A);
+  {
+    TimedScope ts(CX_KERNEL_VERIFY_STATS, s);
+    hipLaunchKernelGGL(verify_stats, dim3(nrows * A.nchunk), dim3(WG), 0, s, A);
+  }
+  TimedScope ts(CX_KERNEL_VERIFY_REST, s);
   hipLaunchKernelGGL(verify_decide, dim3(A.B), dim3(WG), 0, s, A);
   if (any_stochastic) {
     hipLaunchKernelGGL(verify_residual, dim3(A.B * A.nchunk), dim3(WG), 0, s, A);

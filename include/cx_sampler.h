@@ -134,6 +134,20 @@ int cx_spec_verify_host(const float* target, const float* draft, const int32_t* 
                         int32_t* accepted, int32_t* next_tok, int32_t* used,
                         int32_t* row_status);
 
+/* Kernel timing (measurement only).  While enabled, the library records a
+ * hipEvent pair around every launch of the selected kernels, on the stream
+ * the kernel is launched on.  cx_timing_read waits for the recorded events,
+ * returns the summed milliseconds and launch count of one kernel and
+ * forgets its records.  No counterpart in the reference (which has no
+ * device code); callers are benchmarks and profilers. */
+#define CX_KERNEL_SAMPLE        0  /* fused sampler kernel            */
+#define CX_KERNEL_SAMPLE_SLOW   1  /* multi-pass row kernel           */
+#define CX_KERNEL_VERIFY_STATS  2  /* verify: stats over all rows     */
+#define CX_KERNEL_VERIFY_REST   3  /* verify: decide + residual draw  */
+#define CX_KERNEL_SAMPLE_FINISH 4  /* sampler finisher (rows in several slices) */
+int cx_timing_enable(int on);
+int cx_timing_read(int32_t kernel, double* total_ms, int64_t* launches);
+
 /* Thread-local description of the last failure ("" if none). */
 const char* cx_last_error(void);
 
