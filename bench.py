@@ -143,6 +143,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--quick", action="store_true", help="headline workload only")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="also run a plain 512 MiB device copy (torch copy_) 5 times: the "
+                         "reference kernel for scaling FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -201,6 +204,16 @@ def main() -> int:
             other[name] = entry
             del fn
             torch.cuda.empty_cache()
+
+    if args.copy_probe:
+        _say("[bench] copy probe: 5 x 512 MiB device copy")
+        src = torch.ones(128 << 20, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+        torch.cuda.empty_cache()
 
     cpu = None
     if args.cpu_seconds > 0:

@@ -7,6 +7,7 @@
 #include <string>
 
 #include "cx_sampler.h"
+#include "cx_device.hpp"
 #include "cx_internal.hpp"
 #include "cx_timing.hpp"
 
@@ -113,11 +114,10 @@ static int sample_impl(const void* logits, int bf16, int64_t ld, int32_t B, int3
   off += (size_t)16 * CAPW * 4;
   A.off_gather = (int)off;
   off += (size_t)LEAN_CAP * 12;
-  const size_t fin = (size_t)SORT_CAP * (8 + 4 + 4 + 8 + 8);
-  A.fin_lds_bytes = (int)fin;
-  A.lds_bytes = (int)(A.nsplit > 1 ? off : (off > fin ? off : fin));
-  if (A.lds_bytes > 150 * 1024) return fail(CX_EINVAL, "LDS layout too large (%d)", A.lds_bytes);
-  {  // multi-pass kernel: full-row bitmap + hash keys + histogram / gather work area
+  size_t fin = (size_t)SORT_CAP * (8 + 4 + 4 + 8 + 8);
+  {  // multi-pass row path: full-row bitmap + hash keys + histogram / gather
+     // work area + per-thread sums; shares the dynamic LDS of the kernel
+     // that runs it
     long bits = ldh > 0 ? pow2_at_least(V) : 32;
     if (bits > (1 << 18)) bits = 1 << 18;
     A.slow_nbw = (int)(bits / 32 > 1 ? bits / 32 : 1);
@@ -125,9 +125,16 @@ static int sample_impl(const void* logits, int bf16, int64_t ld, int32_t B, int3
     A.slow_off_hkey = (int)so;
     so = align_up(so + (size_t)A.ns * 4, 16);
     A.slow_off_work = (int)so;
-    so += 1024 * 12 + 1024 * 24;
+    so = align_up(so + 1024 * 12 + 1024 * 24, 16);
+    A.slow_off_tsum = (int)so;
+    so += (size_t)WG * 8;
     A.slow_lds_bytes = (int)so;
+    if (so > fin) fin = so;
+    if (so > off) off = so;
   }
+  A.fin_lds_bytes = (int)fin;
+  A.lds_bytes = (int)(A.nsplit > 1 ? off : (off > fin ? off : fin));
+  if (A.lds_bytes > 150 * 1024) return fail(CX_EINVAL, "LDS layout too large (%d)", A.lds_bytes);
   hipStream_t s = (hipStream_t)stream;
   int e = launch_sample(A, s);
   if (e != 0) return hip_fail((hipError_t)e, "sample launch");

@@ -66,8 +66,10 @@ __device__ inline uint64_t kth_candidate_key(const SampleArgs& A, int row, uint6
   return prefix;
 }
 
-__device__ inline void finish_row(const SampleArgs& A, int row, const cx_row_params& P,
-                                  unsigned char* dyn, double* red_d, int* red_i) {
+// Returns false, with nothing written, when the row needs the exact
+// multi-pass path.
+__device__ inline bool finish_row_fast(const SampleArgs& A, int row, const cx_row_params& P,
+                                       unsigned char* dyn, double* red_d, int* red_i) {
   __shared__ int f_n;
   __shared__ int f_j;
   const int t = threadIdx.x;
@@ -78,7 +80,7 @@ __device__ inline void finish_row(const SampleArgs& A, int row, const cx_row_par
 
   if (flags & SF_UNSUPPORTED) {
     write_row_result(A, row, CX_ROW_UNSUPPORTED, -1);
-    return;
+    return true;
   }
   if (P.temperature == 0.0) {                      // sampler.py:114-115
     double bv = -__builtin_inf();
@@ -90,7 +92,7 @@ __device__ inline void finish_row(const SampleArgs& A, int row, const cx_row_par
     int tok = ni != INT_MAX ? ni : (bi == INT_MAX ? 0 : bi);
     write_row_result(A, row, CX_ROW_GREEDY, tok);
     write_one_hot(A, row, tok);
-    return;
+    return true;
   }
 
   const double invT = 1.0 / P.temperature;
@@ -108,13 +110,11 @@ __device__ inline void finish_row(const SampleArgs& A, int row, const cx_row_par
     tau = max(tau, st[s].tau);
     tol = st[s].tol > tol ? st[s].tol : tol;
   }
-  auto pending = [&]() { write_row_result(A, row, ROW_PENDING, -1); };
   // Degenerate rows (NaN / +inf / all -inf), tie floods, typical-p and a
   // possible P**(1/T) underflow (ln V / T > 740) go to the multi-pass kernel.
   if (mnan || !(S > 0.0) || !(S < __builtin_inf()) || (flags & (SF_OVERFLOW | SF_INEXACT)) ||
       P.typical_p < 1.0 || A.logV * invT > 740.0) {
-    pending();
-    return;
+    return false;
   }
   bool region_incomplete_after_shrink = false;
   const bool region_all_pre = tau <= 1u;
@@ -165,7 +165,7 @@ __device__ inline void finish_row(const SampleArgs& A, int row, const cx_row_par
     E = f_n;
     region_incomplete_after_shrink = true;
   }
-  if (E > SORT_CAP || E == 0) { pending(); return; }
+  if (E > SORT_CAP || E == 0) return false;
   block_sort(skey, sidx, saux, E);
 
   const bool region_all = region_all_pre && !region_incomplete_after_shrink;
@@ -183,8 +183,7 @@ __device__ inline void finish_row(const SampleArgs& A, int row, const cx_row_par
       nk = f_j;
       complete = true;
     } else if (!region_all) {
-      pending();
-      return;
+      return false;
     }
   }
   // ---- probabilities of the kept prefix
@@ -208,10 +207,10 @@ __device__ inline void finish_row(const SampleArgs& A, int row, const cx_row_par
       nk = m + 1;
       complete = true;
     } else {
-      if (!complete) { pending(); return; }
+      if (!complete) return false;
       near = fabs(sc[nk - 1] - P.top_p) <= tol * sc[nk - 1];
     }
-    if (near) { pending(); return; }
+    if (near) return false;
   }
   // ---- min-p relative to the top probability
   if (P.min_p > 0.0) {
@@ -222,9 +221,9 @@ __device__ inline void finish_row(const SampleArgs& A, int row, const cx_row_par
       if (sv[j] < floor_p) atomicMin(&f_j, j);
     __syncthreads();
     if (f_j < nk) { nk = f_j; complete = true; }
-    else if (!complete) { pending(); return; }
+    else if (!complete) return false;
   }
-  if (!complete) { pending(); return; }
+  if (!complete) return false;
 
   // ---- normalise and draw in token-id order
   double z = 0.0;
@@ -251,6 +250,14 @@ __device__ inline void finish_row(const SampleArgs& A, int row, const cx_row_par
     for (int j = t; j < nk; j += WG) p[sidx[j]] = (float)(sv[saux[j]] / Z);
   }
   write_row_result(A, row, CX_ROW_OK, tok);
+  return true;
+}
+
+// Finish a row from its slices' statistics and regions; a row this cannot
+// decide is marked pending for the exact multi-pass kernel.
+__device__ inline void finish_row(const SampleArgs& A, int row, const cx_row_params& P,
+                                  unsigned char* dyn, double* red_d, int* red_i) {
+  if (!finish_row_fast(A, row, P, dyn, red_d, red_i)) write_row_result(A, row, ROW_PENDING, -1);
 }
 
 }  // namespace cx

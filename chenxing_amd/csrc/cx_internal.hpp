@@ -22,8 +22,9 @@ constexpr int SF_OVERFLOW = 1;            // a wave buffer flooded with ties
 constexpr int SF_UNSUPPORTED = 2;         // window longer than WIN_MAX
 constexpr int SF_INEXACT = 4;             // the slice's normaliser has no usable error bound
 
-// Internal row_status value: the finisher could not decide the row and the
-// multi-pass kernel must finish it.  Never returned to the caller.
+
+// Internal row_status value: the fused path could not decide the row and
+// the exact multi-pass kernel must finish it.  Never returned to the caller.
 constexpr int ROW_PENDING = 0x40000000;
 
 struct SplitStats {       // one per (row, slice), 64 bytes
@@ -70,7 +71,7 @@ struct SampleArgs {
   int32_t bf16;
   double logV;            // log(V)
   int32_t slow_nbw;       // multi-pass kernel: full-row bitmap words (power of two)
-  int32_t slow_off_hkey, slow_off_work, slow_lds_bytes;
+  int32_t slow_off_hkey, slow_off_work, slow_off_tsum, slow_lds_bytes;
 };
 
 // ---------------------------------------------------------------- verify

@@ -26,7 +26,7 @@
 // region are decided by one wave; other rows write their region and
 // statistics and run finish_row (cx_finish.hpp), in the same workgroup or,
 // for several slices, in finish_kernel.  Rows none of these can decide are
-// marked pending and finished by the multi-pass kernel in cx_slow.hip.
+// marked pending and finished by the exact multi-pass kernel (cx_slow.hip).
 #include "cx_device.hpp"
 #include "cx_sampler.h"
 #include "cx_internal.hpp"
@@ -999,7 +999,8 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   const bool sum_ok = !anynan && rb_ok && Ss > 0.0 && Ss < __builtin_inf() && tol <= TOL_MAX;
   const int nlist = s_cnt;
 
-  // ---- lean finish (one slice, top-k <= 64, short list, nothing exotic)
+  // ---- lean finish (one slice, top-k <= 64, short list, nothing exotic):
+  // wave 0 decides; a row it cannot decide is left pending for the exact path
   if (single && sum_ok && !ovf && P.top_k > 0 && P.top_k <= 64 && P.typical_p >= 1.0 &&
       !A.out_probs && A.logV * invT <= 740.0 && nlist <= LEAN_CAP) {
     if (wave_id() != 0) return;

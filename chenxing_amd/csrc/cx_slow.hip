@@ -1,512 +1,33 @@
-// cx_slow.hip -- exact multi-pass row kernel (reference chenxing/core/sampler.py:63-127).
-//
-// Finishes the rows the fused kernel marked pending: degenerate rows (NaN,
-// +inf, all -inf, P**(1/T) underflow), nuclei or top-k sets deeper than the
-// fused kernel's region, tie floods, top-p decisions within the fused
-// normaliser's error bound, and typical-p.  One workgroup per row; every
-// quantity is fp64 and every selection is exact:
-//
-//   pass A   max / first argmax / first NaN / min of the penalised row
-//   pass B   S = sum exp((x - M) / T)  (and the T = 1 sum for the underflow test)
-//   select   top-k threshold (count select) and the top-p and typical-p cuts
-//            (mass select): histogram passes over an exactly narrowing key
-//            range, then the last bucket is gathered into LDS and sorted
-//   draw     per-thread sums over contiguous id ranges, block scan, and a
-//            sequential scan inside the range that holds u (token-id order)
-//
-// Rows are re-read from memory for every pass; pending rows are rare on the
-// fused path's target workloads.
-#include "cx_device.hpp"
-#include "cx_sampler.h"
-#include "cx_internal.hpp"
+// cx_slow.hip -- launches the exact multi-pass row path (cx_slow.hpp) for
+// the rows the fused sampler left pending.  One workgroup covers
+// SLOW_ROWS_PER_WG rows (one: pending rows run in parallel); a workgroup
+// whose rows are all decided reads their status words once and exits.
+#include "cx_slow.hpp"
 #include "cx_timing.hpp"
 
 namespace cx {
 
-constexpr int NB = 1024;             // histogram buckets per pass
-constexpr int SCAP = 1024;           // gathered bucket capacity
-
-__device__ __forceinline__ uint32_t s_hash_slot(int id, int ns_log2) {
-  return ((uint32_t)id * 0x9E3779B1u) >> (32 - ns_log2);
-}
-
-struct SlowRow {
-  const cx_row_params* P;
-  const void* rowp;
-  int bf16;
-  int V;
-  bool pen;
-  const uint32_t* bitmap;
-  int nbw;
-  const uint32_t* hkey;
-  const float* hval;
-  int ns_log2;
-  double M, invT, S;
-};
-
-__device__ __forceinline__ float raw_at(const SlowRow& R, int i) {
-  return R.bf16 ? __uint_as_float((uint32_t)((const uint16_t*)R.rowp)[i] << 16)
-                : ((const float*)R.rowp)[i];
-}
-
-// Penalised fp64 value of element i (sampler.py:65-72 + presence/frequency).
-__device__ inline double value_at(const SlowRow& R, int i) {
-  float raw = raw_at(R, i);
-  double x = (double)raw;
-  if (R.pen && ((R.bitmap[(i >> 5) & (R.nbw - 1)] >> (i & 31)) & 1u)) {
-    const uint32_t mask = (1u << R.ns_log2) - 1;
-    uint32_t s = s_hash_slot(i, R.ns_log2);
-    for (;;) {
-      uint32_t k = R.hkey[s];
-      if (k == HEMPTY) break;
-      if ((k >> 12) == (uint32_t)i) {
-        const cx_row_params& p = *R.P;
-        if (p.repetition_penalty != 1.0)
-          x = x > 0.0 ? x / p.repetition_penalty : x * p.repetition_penalty;
-        x = x - p.frequency_penalty * (double)(k & 0xFFFu);
-        x = x - p.presence_penalty;
-        break;
-      }
-      s = (s + 1) & mask;
-    }
-  }
-  return x;
-}
-
-__device__ __forceinline__ double mass_of(const SlowRow& R, double v) {
-  return exp((v - R.M) * R.invT) / R.S;
-}
-
-// Boundary of a prefix in (key desc, idx asc) order: element e is inside iff
-// key > k || (key == k && idx <= i).
-struct Cut {
-  uint64_t k;
-  int i;
-};
-__device__ __forceinline__ bool inside(const Cut& c, uint64_t key, int idx) {
-  return key > c.k || (key == c.k && idx <= c.i);
-}
-
-struct Filters {
-  Cut rank;          // top-k / top-p prefix
-  double floor_p;    // min-p floor on P (0 = off)
-  bool typ;          // typical-p cut active
-  double H;          // entropy for the typical order
-  Cut tcut;          // typical prefix in (-shift desc, idx asc) order
-};
-
-__device__ __forceinline__ uint64_t typ_key(double P, double H) {
-  double lp = log(P > 1e-38 ? P : 1e-38);
-  return d2key(-fabs(lp + H));
-}
-
-// Kept by top-k, top-p and min-p (the typical cut is applied separately).
-__device__ __forceinline__ bool kept_rank(const Filters& F, uint64_t key, int idx, double P) {
-  return inside(F.rank, key, idx) && P >= F.floor_p;
-}
-
-struct SlowLds {
-  uint32_t* cnt;     // [NB]
-  double* mass;      // [NB]
-  uint64_t* gk;      // [SCAP]
-  int32_t* gi;       // [SCAP]
-  int32_t* ga;       // [SCAP]
-  double* gm;        // [SCAP]
-};
-
-// Order key of element (v, idx) for a selection: rank order (value) or the
-// typical order (-|log P + H|).  Returns false if the element is not eligible.
-template <bool TYP>
-__device__ __forceinline__ bool sel_key(const SlowRow& R, const Filters& F, int i, double v,
-                                        uint64_t& key, double& m) {
-  uint64_t vk = d2key(v);
-  if (!TYP) {
-    key = vk;
-    m = 0.0;
-    return true;
-  }
-  double P = mass_of(R, v);
-  if (!kept_rank(F, vk, i, P)) return false;
-  key = typ_key(P, F.H);
-  m = P;
-  return true;
-}
-
-// Select the shortest prefix, in (key desc, idx asc) order over the eligible
-// elements, that holds `target` elements (COUNT) or `target` mass (MASS).
-// Returns false if the eligible total never reaches the target.
-template <bool TYP, bool MASS>
-__device__ bool select_prefix(const SlowRow& R, const Filters& F, const Cut& elig, double target,
-                              uint64_t klo, uint64_t khi, SlowLds& L, Cut& out, double* red_d,
-                              int* red_i) {
-  __shared__ uint64_t sh_u[4];
-  __shared__ double sh_d[2];
-  __shared__ int sh_i[2];
-  const int t = threadIdx.x;
-  double above = 0.0;                           // count or mass of elements with key > khi
-  for (int level = 0; level < 8; ++level) {
-    uint64_t D = khi - klo;
-    int sh = 0;
-    while ((D >> sh) >= (uint64_t)NB) ++sh;
-    for (int b = t; b < NB; b += WG) { L.cnt[b] = 0u; L.mass[b] = 0.0; }
-    __syncthreads();
-    for (int i = t; i < R.V; i += WG) {
-      double v = value_at(R, i);
-      uint64_t key;
-      double m;
-      if (!sel_key<TYP>(R, F, i, v, key, m)) continue;
-      if (!TYP && !inside(elig, key, i)) continue;
-      if (key < klo || key > khi) continue;
-      int b = (int)((key - klo) >> sh);
-      atomicAdd(&L.cnt[b], 1u);
-      if (MASS) atomicAdd(&L.mass[b], TYP ? m : mass_of(R, v));
-    }
-    __syncthreads();
-    if (t == 0) {
-      int b = NB - 1;
-      double run = above;
-      bool hit = false;
-      for (; b >= 0; --b) {
-        double w = MASS ? L.mass[b] : (double)L.cnt[b];
-        // only a bucket holding elements can complete the prefix (a target of
-        // 0 selects the first element, as searchsorted(cum, 0) + 1 does)
-        if (L.cnt[b] > 0u && run + w >= target) { hit = true; break; }
-        run += w;
-      }
-      sh_i[0] = hit ? b : -1;
-      sh_i[1] = hit ? (int)L.cnt[b] : 0;
-      sh_d[0] = run;
-    }
-    __syncthreads();
-    const int bstar = sh_i[0];
-    const int nb = sh_i[1];
-    if (bstar < 0) return false;
-    above = sh_d[0];
-    const uint64_t nlo = klo + ((uint64_t)bstar << sh);
-    const uint64_t nhi_raw = nlo + (sh >= 64 ? ~0ull : ((1ull << sh) - 1));
-    const uint64_t nhi = nhi_raw < khi && nhi_raw >= nlo ? nhi_raw : khi;
-    klo = nlo;
-    khi = nhi;
-    __syncthreads();
-    if (nb <= SCAP || klo == khi) {
-      // gather the bucket (for a single-key bucket larger than SCAP only the
-      // lowest ids are needed: the cut falls at a count known from its mass)
-      if (nb > SCAP) {
-        // all share one key (and one mass): how many of them complete the prefix
-        double unit = 0.0;
-        if (t == 0) {
-          unit = MASS ? (L.mass[bstar] / (double)nb) : 1.0;
-          double need = (target - above) / unit;
-          long c = (long)ceil(need);
-          if (c < 1) c = 1;
-          if (c > nb) c = nb;
-          sh_i[0] = (int)c;
-        }
-        __syncthreads();
-        const int c = sh_i[0];
-        // the c-th smallest id among the bucket: count select over ids
-        int lo_id = 0, hi_id = R.V - 1, before = 0;
-        for (int lev = 0; lev < 4; ++lev) {
-          int span = hi_id - lo_id + 1;
-          int ish = 0;
-          while ((span >> ish) >= NB) ++ish;
-          for (int b = t; b < NB; b += WG) L.cnt[b] = 0u;
-          __syncthreads();
-          for (int i = lo_id + t; i <= hi_id; i += WG) {
-            double v = value_at(R, i);
-            uint64_t key;
-            double m;
-            if (!sel_key<TYP>(R, F, i, v, key, m)) continue;
-            if (!TYP && !inside(elig, key, i)) continue;
-            if (key != klo) continue;
-            atomicAdd(&L.cnt[(i - lo_id) >> ish], 1u);
-          }
-          __syncthreads();
-          if (t == 0) {
-            int b = 0, run = before;
-            for (; b < NB - 1; ++b) {
-              if (run + (int)L.cnt[b] >= c) break;
-              run += (int)L.cnt[b];
-            }
-            sh_i[0] = b;
-            sh_i[1] = run;
-          }
-          __syncthreads();
-          before = sh_i[1];
-          lo_id = lo_id + (sh_i[0] << ish);
-          hi_id = min(hi_id, lo_id + (1 << ish) - 1);
-          __syncthreads();
-          if (ish == 0) break;
-        }
-        out.k = klo;
-        out.i = lo_id;
-        return true;
-      }
-      __shared__ int gn;
-      if (t == 0) gn = 0;
-      __syncthreads();
-      for (int i = t; i < R.V; i += WG) {
-        double v = value_at(R, i);
-        uint64_t key;
-        double m;
-        if (!sel_key<TYP>(R, F, i, v, key, m)) continue;
-        if (!TYP && !inside(elig, key, i)) continue;
-        if (key < klo || key > khi) continue;
-        int pos = atomicAdd(&gn, 1);
-        if (pos < SCAP) {
-          L.gk[pos] = key;
-          L.gi[pos] = i;
-          L.gm[pos] = MASS ? (TYP ? m : mass_of(R, v)) : 1.0;
-        }
-      }
-      __syncthreads();
-      const int n = min(gn, SCAP);   // >= 1: the bucket was counted non-empty
-      for (int j = t; j < n; j += WG) L.ga[j] = j;
-      __syncthreads();
-      block_sort(L.gk, L.gi, L.ga, n);
-      if (t == 0) {
-        double run = above;
-        int j = 0;
-        for (; j < n - 1; ++j) {
-          run += L.gm[L.ga[j]];
-          if (run >= target) break;
-        }
-        sh_u[0] = L.gk[j];
-        sh_i[0] = L.gi[j];
-      }
-      __syncthreads();
-      out.k = sh_u[0];
-      out.i = sh_i[0];
-      __syncthreads();
-      return true;
-    }
-  }
-  // unreachable for 64-bit keys (each level narrows the range by NB)
-  out.k = klo;
-  out.i = INT_MAX;
-  return true;
-}
+constexpr int SLOW_ROWS_PER_WG = 1;
 
 __global__ __launch_bounds__(WG) void slow_kernel(SampleArgs A) {
   extern __shared__ __align__(16) unsigned char dyn[];
   __shared__ double red_d[2 * NWAVE + 4];
   __shared__ int red_i[2 * NWAVE + 4];
-  __shared__ double tsum[WG];
-  const int row = blockIdx.x;
-  if (A.row_status[row] != ROW_PENDING) return;
-  const int t = threadIdx.x;
-  const cx_row_params P = A.prm[row];
-  const int V = A.V;
-
-  SlowRow R;
-  R.P = &P;
-  R.bf16 = A.bf16;
-  R.V = V;
-  R.rowp = (const char*)A.logits + (size_t)row * (size_t)A.ld * (A.bf16 ? 2 : 4);
-  // ---- penalty tables for the whole row
-  int wlen = 0, wstart = 0;
-  if (A.ldh > 0) {
-    int len = max(0, min(A.hist_len[row], (int)A.ldh));
-    wstart = P.n_keep > 0 ? max(0, len - max(64, P.n_keep)) : 0;
-    wlen = len - wstart;
+  __shared__ uint32_t s_pending;
+  const int row0 = blockIdx.x * SLOW_ROWS_PER_WG;
+  if (threadIdx.x < 64) {
+    const int r = row0 + (int)threadIdx.x;
+    const bool p = threadIdx.x < SLOW_ROWS_PER_WG && r < A.B && A.row_status[r] == ROW_PENDING;
+    const uint64_t b = __ballot(p);
+    if (threadIdx.x == 0) s_pending = (uint32_t)b;
   }
-  R.pen = wlen > 0 && (P.repetition_penalty != 1.0 || P.presence_penalty != 0.0 ||
-                       P.frequency_penalty != 0.0);
-  uint32_t* bitmap = (uint32_t*)dyn;
-  uint32_t* hkey = (uint32_t*)(dyn + A.slow_off_hkey);
-  R.bitmap = bitmap;
-  R.hkey = hkey;
-  R.hval = nullptr;
-  R.nbw = A.slow_nbw;
-  R.ns_log2 = A.ns_log2;
-  if (R.pen) {
-    for (int i = t; i < R.nbw; i += WG) bitmap[i] = 0u;
-    for (int i = t; i < A.ns; i += WG) hkey[i] = HEMPTY;
-    __syncthreads();
-    const int32_t* hrow = A.hist + (size_t)row * A.ldh;
-    for (int i = t; i < wlen; i += WG) {
-      int id = hrow[wstart + i];
-      if (id >= 0 && id < V) {
-        atomicOr(&bitmap[(id >> 5) & (R.nbw - 1)], 1u << (id & 31));
-        const uint32_t mask = (1u << A.ns_log2) - 1;
-        uint32_t s = s_hash_slot(id, A.ns_log2);
-        for (;;) {
-          uint32_t old = atomicCAS(&hkey[s], HEMPTY, ((uint32_t)id << 12) | 1u);
-          if (old == HEMPTY) break;
-          if ((old >> 12) == (uint32_t)id) { atomicAdd(&hkey[s], 1u); break; }
-          s = (s + 1) & mask;
-        }
-      }
-    }
-    __syncthreads();
-  }
-  SlowLds L;
-  unsigned char* base = dyn + A.slow_off_work;
-  L.cnt = (uint32_t*)base;
-  L.mass = (double*)(base + NB * 4);
-  L.gk = (uint64_t*)(base + NB * 12);
-  L.gi = (int32_t*)(base + NB * 12 + SCAP * 8);
-  L.ga = (int32_t*)(base + NB * 12 + SCAP * 12);
-  L.gm = (double*)(base + NB * 12 + SCAP * 16);
-
-  // ---- pass A: max, min, first argmax, first NaN
-  double mx = -__builtin_inf(), mn = __builtin_inf();
-  int bi = INT_MAX, ni = INT_MAX;
-  double bv = -__builtin_inf();
-  for (int i = t; i < V; i += WG) {
-    double v = value_at(R, i);
-    if (v != v) { ni = min(ni, i); continue; }
-    argmax_merge(bv, bi, v, i);
-    mx = v > mx ? v : mx;
-    mn = v < mn ? v : mn;
-  }
-  block_argmax(bv, bi, red_d, red_i);
-  ni = block_min(ni, red_i, INT_MAX);
-  mx = bv;
-  mn = block_min(mn, red_d, __builtin_inf());
-  const int amax = ni != INT_MAX ? ni : (bi == INT_MAX ? 0 : bi);
-  const double invT = 1.0 / P.temperature;
-  bool degenerate = ni != INT_MAX || mx == __builtin_inf() || mx == -__builtin_inf();
-  R.M = mx;
-  R.invT = invT;
-  R.S = 1.0;
-  // ---- pass B: the normaliser (and the T = 1 sum for the P**(1/T) underflow)
-  if (!degenerate) {
-    const bool under = P.temperature != 1.0 && log((double)V) * invT > 740.0;
-    double s = 0.0, s1 = 0.0;
-    for (int i = t; i < V; i += WG) {
-      double v = value_at(R, i);
-      s += exp((v - mx) * invT);
-      if (under) s1 += exp(v - mx);
-    }
-    R.S = block_sum(s, red_d);
-    if (under) {
-      double S1 = block_sum(s1, red_d);
-      if (pow(1.0 / S1, invT) == 0.0) degenerate = true;
-    }
-  }
-  if (degenerate) {
-    // all-NaN probabilities: top-k or min-p zero them and argmax(x) follows
-    // (sampler.py:123-125); otherwise numpy's choice raises ValueError.
-    const bool am = P.top_k > 0 || P.min_p > 0.0;
-    if (A.out_probs) {
-      float* pr = A.out_probs + (size_t)row * V;
-      for (int i = t; i < V; i += WG) pr[i] = (am && i == amax) ? 1.0f : 0.0f;
-    }
-    if (t == 0) {
-      A.out_id[row] = am ? amax : -1;
-      A.row_status[row] = (am ? CX_ROW_ARGMAX : CX_ROW_ERROR) | CX_ROW_FLAG_SLOW;
-    }
-    return;
-  }
-
-  // ---- rank-order filters
-  Filters F;
-  F.rank.k = 0;
-  F.rank.i = INT_MAX;
-  F.floor_p = 0.0;
-  F.typ = false;
-  F.H = 0.0;
-  const uint64_t kmax = d2key(mx), kmin = d2key(mn);
-  Cut all;
-  all.k = 0;
-  all.i = INT_MAX;
-  if (P.top_k > 0 && P.top_k < V) {                          // sampler.py:76-79
-    Cut c;
-    select_prefix<false, false>(R, F, all, (double)P.top_k, kmin, kmax, L, c, red_d, red_i);
-    F.rank.k = c.k;                                          // ties at the k-th value stay
-    F.rank.i = INT_MAX;
-  }
-  if (P.top_p < 1.0) {                                       // sampler.py:81-89
-    Cut c;
-    const uint64_t lo = F.rank.k > kmin ? F.rank.k : kmin;
-    if (select_prefix<false, true>(R, F, F.rank, P.top_p, lo, kmax, L, c, red_d, red_i))
-      F.rank = c;
-  }
-  if (P.min_p > 0.0) F.floor_p = P.min_p * (1.0 / R.S);      // sampler.py:91-93
-  if (P.typical_p < 1.0) {                                   // sampler.py:95-105
-    double h = 0.0;
-    uint64_t tlo = ~0ull, thi = 0ull;
-    for (int i = t; i < V; i += WG) {
-      double v = value_at(R, i);
-      double p = mass_of(R, v);
-      if (!kept_rank(F, d2key(v), i, p)) continue;
-      h -= p * log(p > 1e-38 ? p : 1e-38);
-    }
-    F.H = block_sum(h, red_d);
-    for (int i = t; i < V; i += WG) {
-      double v = value_at(R, i);
-      double p = mass_of(R, v);
-      if (!kept_rank(F, d2key(v), i, p)) continue;
-      uint64_t k = typ_key(p, F.H);
-      tlo = k < tlo ? k : tlo;
-      thi = k > thi ? k : thi;
-    }
-    tlo = block_min<unsigned long long>(tlo, (unsigned long long*)red_d, ~0ull);
-    thi = block_max<unsigned long long>(thi, (unsigned long long*)red_d, 0ull);
-    Cut c;
-    F.typ = select_prefix<true, true>(R, F, all, P.typical_p, tlo, thi, L, c, red_d, red_i);
-    F.tcut = c;
-  }
-
-  // ---- normalise and draw in token-id order (sampler.py:123-127)
-  auto kept_mass = [&](int i) -> double {
-    double v = value_at(R, i);
-    double p = mass_of(R, v);
-    uint64_t k = d2key(v);
-    if (!kept_rank(F, k, i, p)) return 0.0;
-    if (F.typ && !inside(F.tcut, typ_key(p, F.H), i)) return 0.0;
-    return p;
-  };
-  const int per = (V + WG - 1) / WG;
-  const int e0 = min(V, t * per), e1 = min(V, e0 + per);
-  double s = 0.0;
-  for (int i = e0; i < e1; ++i) s += kept_mass(i);
-  tsum[t] = s;
-  const double Z = block_sum(s, red_d);
-  if (!(Z > 0.0)) {
-    if (A.out_probs) {
-      float* pr = A.out_probs + (size_t)row * V;
-      for (int i = t; i < V; i += WG) pr[i] = i == amax ? 1.0f : 0.0f;
-    }
-    if (t == 0) {
-      A.out_id[row] = amax;
-      A.row_status[row] = CX_ROW_ARGMAX | CX_ROW_FLAG_SLOW;
-    }
-    return;
-  }
-  // cdf_i = cumsum(P / Z)_i / cumsum(P / Z)_last; first i with cdf_i > u
-  for (int j = t; j < WG; j += WG) tsum[j] = tsum[j] / Z;
   __syncthreads();
-  block_scan(tsum, WG, red_d);
-  const double last = tsum[WG - 1];
-  const double u = A.u[row];
-  const double prev = t > 0 ? tsum[t - 1] : 0.0;
-  int found = INT_MAX;
-  if (prev / last <= u && tsum[t] / last > u) {
-    double run = prev;
-    for (int i = e0; i < e1; ++i) {
-      double q = kept_mass(i);
-      if (q == 0.0) continue;
-      run += q / Z;
-      if (run / last > u) { found = i; break; }
-    }
-  }
-  found = block_min(found, red_i, INT_MAX);
-  if (found == INT_MAX) {
-    // u beyond the last step by rounding: the last kept id
-    int lastk = -1;
-    for (int i = t; i < V; i += WG)
-      if (kept_mass(i) > 0.0) lastk = max(lastk, i);
-    found = block_max(lastk, red_i, -1);
-  }
-  if (A.out_probs) {
-    float* pr = A.out_probs + (size_t)row * V;
-    for (int i = t; i < V; i += WG) pr[i] = (float)(kept_mass(i) / Z);
-  }
-  if (t == 0) {
-    A.out_id[row] = found;
-    A.row_status[row] = CX_ROW_OK | CX_ROW_FLAG_SLOW;
+  uint32_t pend = s_pending;
+  while (pend) {
+    const int j = __builtin_ctz(pend);
+    pend &= pend - 1;
+    slow_row(A, row0 + j, dyn, red_d, red_i);
+    __syncthreads();
   }
 }
 
@@ -520,7 +41,8 @@ int launch_slow(const SampleArgs& A, hipStream_t s) {
     attr = A.slow_lds_bytes;
   }
   TimedScope ts(CX_KERNEL_SAMPLE_SLOW, s);
-  hipLaunchKernelGGL(slow_kernel, dim3(A.B), dim3(WG), A.slow_lds_bytes, s, A);
+  const int grid = (A.B + SLOW_ROWS_PER_WG - 1) / SLOW_ROWS_PER_WG;
+  hipLaunchKernelGGL(slow_kernel, dim3(grid), dim3(WG), A.slow_lds_bytes, s, A);
   return (int)hipGetLastError();
 }
 

@@ -38,7 +38,7 @@ extern "C" {
 #define CX_ROW_ERROR       3  /* reference raises ValueError (NaN probabilities in choice) */
 #define CX_ROW_UNSUPPORTED 4  /* input outside the library's limits (history window) */
 /* row_status high bits: how the row was computed (informational) */
-#define CX_ROW_FLAG_SLOW   0x100  /* resolved by the multi-pass row kernel */
+#define CX_ROW_FLAG_SLOW   0x100  /* resolved by the exact multi-pass row path */
 #define CX_ROW_FLAG_EXACT  0x200  /* normaliser recomputed in fp64 for a near-threshold decision */
 
 /* Per-row sampling parameters, 64 bytes.  Mirrors SamplingParams
@@ -141,7 +141,7 @@ int cx_spec_verify_host(const float* target, const float* draft, const int32_t* 
  * forgets its records.  No counterpart in the reference (which has no
  * device code); callers are benchmarks and profilers. */
 #define CX_KERNEL_SAMPLE        0  /* fused sampler kernel            */
-#define CX_KERNEL_SAMPLE_SLOW   1  /* multi-pass row kernel           */
+#define CX_KERNEL_SAMPLE_SLOW   1  /* exact multi-pass row kernel     */
 #define CX_KERNEL_VERIFY_STATS  2  /* verify: stats over all rows     */
 #define CX_KERNEL_VERIFY_REST   3  /* verify: decide + residual draw  */
 #define CX_KERNEL_SAMPLE_FINISH 4  /* sampler finisher (rows in several slices) */
