@@ -107,6 +107,8 @@ static int sample_impl(const void* logits, int bf16, int64_t ld, int32_t B, int3
   A.off_hword = (int)off;
   off += (size_t)nslot * 4;
   A.off_hval = (int)off;
+  off += (size_t)nslot * 4;
+  A.off_hpen = (int)off;
   off = align_up(off + (size_t)nslot * 4, 16);
   A.off_wkey = (int)off;
   off += (size_t)16 * CAPW * 4;

@@ -49,6 +49,7 @@ struct PenIndex {
   CX_LDS uint32_t* bitmap;
   CX_LDS uint32_t* hword;
   CX_LDS float* hval;
+  CX_LDS float* hpen;     // penalised value rounded to fp32 (region pre-test)
   int nbw;
   int ns, ns_log2;
 };
@@ -138,7 +139,9 @@ __device__ __forceinline__ void load_chunk(__amdgpu_buffer_rsrc_t rs, int ch,
                                            typename Elem<BF16>::V (&q)[Elem<BF16>::U]) {
   constexpr int U = Elem<BF16>::U;
 #pragma unroll
-  for (int u = 0; u < U; ++u) q[u] = bload<BF16>(rs, lane_id() * 16, (ch * 64 * U + u * 64) * 16);
+  for (int u = 0; u < U; ++u)
+    q[u] = bload<BF16>(rs, lane_id() * 16,
+                       __builtin_amdgcn_readfirstlane((ch * 64 * U + u * 64) * 16));
 }
 // Next chunk for this wave from the workgroup's counter.
 __device__ __forceinline__ int next_chunk(CX_LDS int* counter) {
@@ -323,60 +326,75 @@ __device__ __forceinline__ void publish(uint32_t ck, int krow, int pub_r, CX_LDS
 
 // ------------------------------------------------------------ stochastic stream
 // The sum is taken against a per-lane integer exponent R: terms
-// exp2(x * c - R) stay finite while x <= top = (value that set R) + 32 / c,
+// exp2(x * c - R) stay finite while x <= top = (value that set R) + LIM / c,
 // so R moves only on such a jump, and the fp64 sum is then rescaled by an
-// exact power of two.  The fp32 argument of a term is within half an ulp of
-// 64 of the exact one, so a term is within TOL_T of its exact value.
+// exact power of two.  A term's fp32 argument is within half an ulp of LIM
+// of the exact one and the 16 terms of a chunk are added in fp32 (15
+// roundings) before the fp64 accumulation, so every term is within TOL_T
+// of its exact value.
+constexpr float LIM = 16.0f;
 struct SState {
   float R;      // integer-valued exponent offset (-inf before the first value)
+  float nR;     // -R, clamped finite (so -inf values give 0 terms before the first value)
   float top;
   double s;
 };
 
+// max of three floats without the NaN quieting fmaxf adds (the stream's sum
+// turns NaN on any NaN element anyway)
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
 template <int NE>
-__device__ __forceinline__ void sum_terms(const float (&x)[NE], float vmax, float c, float lim,
-                                          SState& st) {
+__device__ __forceinline__ float vec_max(const float (&x)[NE]) {
+  if constexpr (NE == 1) {
+    return x[0];
+  } else {
+    float m = max3f(x[0], x[1], x[NE > 2 ? 2 : 1]);
+#pragma unroll
+    for (int j = 3; j < NE; j += 2) m = max3f(m, x[j], x[j + 1 < NE ? j + 1 : j]);
+    return m;
+  }
+}
+
+__device__ __forceinline__ void rescale(float vmax, float c, float lim, SState& st) {
   if (vmax > st.top) {
     // vmax * c may overflow to +inf: R = +inf, the row's sum turns NaN or 0
     // and the row goes to the multi-pass kernel
     const float Rn = __builtin_ceilf(vmax * c);
     if (st.s != 0.0) st.s = __builtin_ldexp(st.s, (int)fmaxf(st.R - Rn, -2048.0f));
     st.R = Rn;
+    st.nR = fminf(-Rn, 3.402823466e38f);
     st.top = vmax + lim;
   }
-  const float nR = fminf(-st.R, 3.402823466e38f);   // finite while R is -inf
-  float ts = __builtin_amdgcn_exp2f(__builtin_fmaf(x[0], c, nR));
-#pragma unroll
-  for (int j = 1; j < NE; ++j) ts += __builtin_amdgcn_exp2f(__builtin_fmaf(x[j], c, nR));
-  st.s += (double)ts;
 }
 
-// Append the candidates of one chunk (some lane of the wave has one; bit u
-// of cm: vector u of this lane reaches the threshold).  With room for every
-// element of every flagged vector, lanes append on their own through the LDS
+// Append the candidates of one chunk (some lane of the wave has one: its
+// chunk maximum reaches the threshold).  With room for all 64 x U x NE
+// elements of the flagged lanes, lanes append on their own through the LDS
 // counter; otherwise the element slots go through wave_insert1 one by one.
 // Penalised elements never enter: their penalised values join afterwards.
 template <bool BF16>
-__device__ __forceinline__ void append_chunk(WaveBuf& wb, const typename Elem<BF16>::V (&q)[Elem<BF16>::U],
-                                             uint32_t cm, int vb, int nv, int lo, bool pen_on,
+__device__ __forceinline__ void append_chunk(WaveBuf& wb,
+                                             const float (&xs)[Elem<BF16>::U][Elem<BF16>::NE],
+                                             bool flagged, int vb, int nv, int lo, bool pen_on,
                                              const PenIndex& X, bool share, uint32_t& ck) {
   using E = Elem<BF16>;
   constexpr int NE = E::NE;
   constexpr int U = E::U;
-  int bound = 0;
+  const int lanes = __popcll(ballot(flagged));
+  if (wb.n + lanes * U * NE <= CAPW) {
+    if (flagged) {
 #pragma unroll
-  for (int u = 0; u < U; ++u) bound += __popcll(ballot((cm >> u) & 1u));
-  if (wb.n + bound * NE <= CAPW) {
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (!ballot((cm >> u) & 1u)) continue;
-      if ((cm >> u) & 1u) {
-        float x[NE];
-        E::unpack(q[u], x);
-        const int e0 = (vb + u * 64) * NE + lo;
+      for (int u = 0; u < U; ++u) {
+        const float (&x)[NE] = xs[u];
+        const int vi = vb + u * 64;
+        const int e0 = vi * NE + lo;
 #pragma unroll
         for (int j = 0; j < NE; ++j) {
-          if (x[j] >= wb.tauf && !(pen_on && pen_bit(X, e0 + j - lo))) {
+          if (vi < nv && x[j] >= wb.tauf && !(pen_on && pen_bit(X, e0 + j - lo))) {
             const uint32_t k = f2key(x[j]);
             const int pos = __hip_atomic_fetch_add(wb.cnt, 1, CX_RELAXED_WG);
             wb.key[pos] = k;
@@ -390,8 +408,7 @@ __device__ __forceinline__ void append_chunk(WaveBuf& wb, const typename Elem<BF
   } else {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      float x[NE];
-      E::unpack(q[u], x);
+      const float (&x)[NE] = xs[u];
       const int vi = vb + u * 64;
       const bool valid = vi < nv;
       const int e0 = vi * NE + lo;
@@ -407,11 +424,14 @@ __device__ __forceinline__ void append_chunk(WaveBuf& wb, const typename Elem<BF
 }
 
 // Stream the vectors of a stochastic slice.  Vector i covers elements
-// lo + i*NE .. lo + i*NE + NE-1, i < nv; q holds this wave's first chunk
-// (chunk wave_id()), loaded by the caller.
+// lo + i*NE .. lo + i*NE + NE-1, i < nv.  q and qn hold this wave's first
+// two chunks (wave_id() and wave_id() + NWAVE), loaded by the caller; every
+// iteration processes q and then asks for the chunk after qn, so two chunks
+// stay in flight.
 template <bool BF16>
 __device__ __forceinline__ void stream_stoch(__amdgpu_buffer_rsrc_t rs,
-                                             typename Elem<BF16>::V (&q)[Elem<BF16>::U], int nv,
+                                             typename Elem<BF16>::V (&q)[Elem<BF16>::U],
+                                             typename Elem<BF16>::V (&qn)[Elem<BF16>::U], int nv,
                                              int lo, bool pen_on, const PenIndex& X, float c,
                                              int krow, int pub_r, CX_LDS int* chunk_ctr,
                                              CX_LDS uint32_t* slots, CX_LDS uint32_t* w_pub,
@@ -420,48 +440,40 @@ __device__ __forceinline__ void stream_stoch(__amdgpu_buffer_rsrc_t rs,
   constexpr int NE = E::NE;
   constexpr int U = E::U;
   constexpr int CH = 64 * U;
-  const float lim = 32.0f / c;
+  const float lim = LIM / c;
   const bool share = true;
   const int nch = (nv + CH - 1) / CH;
   const int nfull = nv / CH;
-  int ch = wave_id();
-  int cn = ch < nch ? next_chunk(chunk_ctr) : nch;
+  // chunk ids are wave-uniform (SGPRs): readfirstlane keeps the buffer
+  // offsets scalar
+  int ch = __builtin_amdgcn_readfirstlane(wave_id());
+  int cn = ch + NWAVE;
   bool fresh = false;              // appended since the last publication
   for (int it = 0; ch < nch; ++it) {
-    typename E::V qn[U];
-    if (cn < nch) load_chunk<BF16>(rs, cn, qn);
-    const int cnn = cn < nch ? next_chunk(chunk_ctr) : nch;
     raise_tau(wb, lds_load(wb.shared));
     const int vb = ch * CH + lane_id();
-    uint32_t cm = 0u;
-    if (ch < nfull) {
+    float x[U][NE];
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        float x[NE];
-        E::unpack(q[u], x);
-        float vmax = x[0];
+    for (int u = 0; u < U; ++u) E::unpack(q[u], x[u]);
+    if (ch >= nfull) {                 // the last, partial chunk
 #pragma unroll
-        for (int j = 1; j < NE; ++j) vmax = fmaxf(vmax, x[j]);
-        sum_terms<NE>(x, vmax, c, lim, st);
-        cm |= (vmax >= wb.tauf ? 1u : 0u) << u;
-      }
-    } else {
+      for (int u = 0; u < U; ++u)
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const bool valid = vb + u * 64 < nv;
-        float x[NE];
-        E::unpack(q[u], x);
-#pragma unroll
-        for (int j = 0; j < NE; ++j) x[j] = valid ? x[j] : -__builtin_inff();
-        float vmax = x[0];
-#pragma unroll
-        for (int j = 1; j < NE; ++j) vmax = fmaxf(vmax, x[j]);
-        sum_terms<NE>(x, vmax, c, lim, st);
-        cm |= (valid && vmax >= wb.tauf ? 1u : 0u) << u;
-      }
+        for (int j = 0; j < NE; ++j) x[u][j] = vb + u * 64 < nv ? x[u][j] : -__builtin_inff();
     }
-    if (ballot(cm != 0u)) {
-      append_chunk<BF16>(wb, q, cm, vb, nv, lo, pen_on, X, share, ck);
+    float cmax = vec_max<NE>(x[0]);
+#pragma unroll
+    for (int u = 1; u < U; ++u) cmax = fmaxf(cmax, vec_max<NE>(x[u]));
+    rescale(cmax, c, lim, st);
+    float ts = 0.0f;
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int j = 0; j < NE; ++j) ts += __builtin_amdgcn_exp2f(__builtin_fmaf(x[u][j], c, st.nR));
+    st.s += (double)ts;
+    const bool flagged = cmax >= wb.tauf;
+    if (ballot(flagged)) {
+      append_chunk<BF16>(wb, x, flagged, vb, nv, lo, pen_on, X, share, ck);
       fresh = true;
     }
     if ((it == 1 || it == 3) && fresh) {
@@ -469,8 +481,11 @@ __device__ __forceinline__ void stream_stoch(__amdgpu_buffer_rsrc_t rs,
       raise_tau(wb, lds_load(wb.shared));
       fresh = false;
     }
+    // next: q <- qn, and the chunk after it into qn
+    const int cnn = cn < nch ? __builtin_amdgcn_readfirstlane(next_chunk(chunk_ctr)) : nch;
 #pragma unroll
     for (int u = 0; u < U; ++u) q[u] = qn[u];
+    if (cnn < nch) load_chunk<BF16>(rs, cnn, qn);
     ch = cn;
     cn = cnn;
   }
@@ -483,13 +498,14 @@ __device__ __forceinline__ void stream_scalar(const char* rowp, int s0, int lo, 
                                               bool pen_on, const PenIndex& X, float c, bool share,
                                               SState& st, WaveBuf& wb, uint32_t& ck) {
   using E = Elem<BF16>;
-  const float lim = 32.0f / c;
+  const float lim = LIM / c;
   for (int e = s0 + lane_id() + 64 * wave_id(); e - lane_id() < hi; e += WG) {
     const bool valid = e < hi;
-    float x1[1] = {valid ? E::scalar(rowp, e) : -__builtin_inff()};
-    sum_terms<1>(x1, x1[0], c, lim, st);
+    const float x = valid ? E::scalar(rowp, e) : -__builtin_inff();
+    rescale(x, c, lim, st);
+    st.s += (double)__builtin_amdgcn_exp2f(__builtin_fmaf(x, c, st.nR));
     uint32_t k = 0u;
-    if (valid && x1[0] >= wb.tauf && !(pen_on && pen_bit(X, e - lo))) k = f2key(x1[0]);
+    if (valid && x >= wb.tauf && !(pen_on && pen_bit(X, e - lo))) k = f2key(x);
     if (ballot(k != 0u)) {
       wb.n = lds_load(wb.cnt);
       if (wave_insert1(wb, k, e, share)) ck = k > ck ? k : ck;
@@ -527,7 +543,8 @@ __device__ __forceinline__ void greedy_vec(const float (&x)[NE], int e0, bool va
 
 template <bool BF16>
 __device__ __forceinline__ void stream_greedy(const char* rowp, __amdgpu_buffer_rsrc_t rs,
-                                              typename Elem<BF16>::V (&q)[Elem<BF16>::U], int nv,
+                                              typename Elem<BF16>::V (&q)[Elem<BF16>::U],
+                                              typename Elem<BF16>::V (&qn)[Elem<BF16>::U], int nv,
                                               int lo, int hi, int s0, bool pen_on,
                                               const PenIndex& X, CX_LDS int* chunk_ctr,
                                               GreedyState& gs) {
@@ -536,12 +553,9 @@ __device__ __forceinline__ void stream_greedy(const char* rowp, __amdgpu_buffer_
   constexpr int U = E::U;
   constexpr int CH = 64 * U;
   const int nch = (nv + CH - 1) / CH;
-  int ch = wave_id();
-  int cn = ch < nch ? next_chunk(chunk_ctr) : nch;
+  int ch = __builtin_amdgcn_readfirstlane(wave_id());
+  int cn = ch + NWAVE;
   while (ch < nch) {
-    typename E::V qn[U];
-    if (cn < nch) load_chunk<BF16>(rs, cn, qn);
-    const int cnn = cn < nch ? next_chunk(chunk_ctr) : nch;
     const int vb = ch * CH + lane_id();
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -550,8 +564,10 @@ __device__ __forceinline__ void stream_greedy(const char* rowp, __amdgpu_buffer_
       const int vi = vb + u * 64;
       greedy_vec<NE>(x, vi * NE + lo, vi < nv, lo, pen_on, X, gs);
     }
+    const int cnn = cn < nch ? __builtin_amdgcn_readfirstlane(next_chunk(chunk_ctr)) : nch;
 #pragma unroll
     for (int u = 0; u < U; ++u) q[u] = qn[u];
+    if (cnn < nch) load_chunk<BF16>(rs, cnn, qn);
     ch = cn;
     cn = cnn;
   }
@@ -701,6 +717,15 @@ __device__ inline bool lean_decide(const SampleArgs& A, int row, const cx_row_pa
   return true;
 }
 
+// ------------------------------------------------------------ penalty corrections
+// Per wave: the sum of the raw and the penalised terms of the window ids its
+// threads own, against the wave's integer exponent offset Rc (every term
+// <= 1), and the largest penalised value.
+struct PenRec {
+  double corr, pr, pmx, Rc;
+  int fl, pad;
+};
+
 // ------------------------------------------------------------ the kernel
 template <bool BF16>
 __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
@@ -711,10 +736,12 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   extern __shared__ __align__(16) unsigned char dyn[];
   __shared__ double red_d[2 * NWAVE + 4];
   __shared__ int red_i[2 * NWAVE + 4];
-  __shared__ double w_s[NWAVE], w_pr[NWAVE], w_corr[NWAVE], w_pmx[NWAVE], w_Rc[NWAVE];
+  __shared__ double w_s[NWAVE];
+  __shared__ PenRec s_pen[NWAVE];
   __shared__ float w_R[NWAVE];
   __shared__ uint32_t w_tau[NWAVE], w_kmx[NWAVE];
   __shared__ int w_fl[NWAVE];
+  __shared__ int s_done;
   __shared__ int w_cnt[NWAVE];
   __shared__ uint32_t s_shared;
   __shared__ uint32_t w_pub[NWAVE];
@@ -726,9 +753,12 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   const int row = blockIdx.x / A.nsplit;
   const int split = blockIdx.x % A.nsplit;
   const int t = threadIdx.x;
-  const cx_row_params P = A.prm[row];
+  // the row's parameters live in LDS after the first barrier (P), not in
+  // registers across the stream; P0 serves the prologue
+  __shared__ cx_row_params sP;
+  const cx_row_params P0 = A.prm[row];
   const double u_row = A.u[row];
-  const bool greedy = P.temperature == 0.0;
+  const bool greedy = P0.temperature == 0.0;
   const int lo = split * A.split_len;
   const int hi = min(A.V, lo + A.split_len);
   const char* rowp = (const char*)A.logits + (size_t)row * (size_t)A.ld * (BF16 ? 2 : 4);
@@ -737,11 +767,11 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   int wlen = 0, wstart = 0;
   if (A.ldh > 0) {
     int len = max(0, min(A.hist_len[row], (int)A.ldh));
-    wstart = P.n_keep > 0 ? max(0, len - max(64, P.n_keep)) : 0;
+    wstart = P0.n_keep > 0 ? max(0, len - max(64, P0.n_keep)) : 0;
     wlen = len - wstart;
   }
-  const bool pen_on = wlen > 0 && (P.repetition_penalty != 1.0 || P.presence_penalty != 0.0 ||
-                                   P.frequency_penalty != 0.0);
+  const bool pen_on = wlen > 0 && (P0.repetition_penalty != 1.0 || P0.presence_penalty != 0.0 ||
+                                   P0.frequency_penalty != 0.0);
   SplitStats* my = A.stats + (size_t)row * A.nsplit + split;
   Cand* mycand = A.cands + ((size_t)row * A.nsplit + split) * CAPS;
 
@@ -750,14 +780,13 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
       my->flags = SF_UNSUPPORTED; my->ncand = 0; my->tau = 1u;
       my->m = 0; my->s = 0; my->tol = 0; my->best_i = INT_MAX; my->nan_i = INT_MAX;
     }
-    if (!single) return;
-    __syncthreads();
-    finish_row(A, row, P, dyn, red_d, red_i);
+    if (single) write_row_result(A, row, CX_ROW_UNSUPPORTED, -1);
     return;
   }
 
-  // the window ids first, then this wave's first chunk: both are in flight
-  // while the index tables are cleared
+  // the window ids first, then this wave's first two chunks (wave_id and
+  // wave_id + NWAVE; the LDS counter hands out the rest from 2 * NWAVE on):
+  // all in flight while the index tables are cleared
   int32_t hid[HPT];
 #pragma unroll
   for (int k = 0; k < HPT; ++k) {
@@ -767,17 +796,20 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   const int nv = A.vec_ok ? (hi - lo) / NE : 0;       // whole vectors of the slice
   const int s0 = lo + nv * NE;                         // first scalar element
   const __amdgpu_buffer_rsrc_t rs = row_rsrc(rowp + (size_t)lo * (BF16 ? 2 : 4), nv * 16);
-  typename E::V q[U];
-  if (wave_id() * CH < nv) load_chunk<BF16>(rs, wave_id(), q);
+  const int ch0 = __builtin_amdgcn_readfirstlane(wave_id());
+  typename E::V q[U], qn[U];
+  if (ch0 * CH < nv) load_chunk<BF16>(rs, ch0, q);
+  if ((ch0 + NWAVE) * CH < nv) load_chunk<BF16>(rs, ch0 + NWAVE, qn);
 
   PenIndex X;
   X.bitmap = to_lds((uint32_t*)(dyn + A.off_bitmap));
   X.hword = to_lds((uint32_t*)(dyn + A.off_hword));
   X.hval = to_lds((float*)(dyn + A.off_hval));
+  X.hpen = to_lds((float*)(dyn + A.off_hpen));
   X.nbw = (hi - lo + 31) >> 5;
   X.ns = pen_on ? A.ns : 0;
   X.ns_log2 = A.ns_log2;
-  if (t == 0) { s_shared = 1u; s_chunk = NWAVE; s_cnt = 0; }
+  if (t == 0) { s_shared = 1u; s_chunk = 2 * NWAVE; s_cnt = 0; s_done = 0; sP = P0; }
   if (t < NWAVE) { w_pub[t] = 0u; w_cnt[t] = 0; }
   if (t < 4 * NWAVE) slots[t] = 0u;
   if (pen_on) {
@@ -785,10 +817,15 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
     for (int i = t; i < X.ns; i += WG) X.hword[i] = HW_EMPTY;
   }
   __syncthreads();
+  const cx_row_params& P = sP;
   // index the window ids of this slice; the thread that inserts a distinct
-  // id owns it and fetches its raw logit (not waited for until the end)
+  // id owns it and fetches its raw logit (stored to the index before the
+  // stream starts)
   int hslot[HPT];
   float gval[HPT];
+#pragma unroll
+  for (int k = 0; k < HPT; ++k)
+    gval[k] = (!greedy && hid[k] >= lo && hid[k] < hi) ? E::scalar(rowp, hid[k]) : 0.0f;
 #pragma unroll
   for (int k = 0; k < HPT; ++k) {
     const int id = hid[k];
@@ -800,23 +837,23 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
       if (created) hslot[k] = h;
     }
   }
-#pragma unroll
-  for (int k = 0; k < HPT; ++k) gval[k] = hslot[k] >= 0 ? E::scalar(rowp, hid[k]) : 0.0f;
   __syncthreads();
 
   // ---------------------------------------------------------------- greedy
   if (greedy) {
     GreedyState gs{-__builtin_inff(), INT_MAX, INT_MAX};
-    stream_greedy<BF16>(rowp, rs, q, nv, lo, hi, s0, pen_on, X, to_lds(&s_chunk), gs);
+    stream_greedy<BF16>(rowp, rs, q, qn, nv, lo, hi, s0, pen_on, X, to_lds(&s_chunk), gs);
     double bv = gs.bi == INT_MAX ? -__builtin_inf() : (double)gs.bv;
     int bi = gs.bi;
     int ni = gs.nan_i;
-#pragma unroll
-    for (int k = 0; k < HPT; ++k) {
-      if (hslot[k] < 0) continue;
-      const double xp = penalise(gval[k], (int)(X.hword[hslot[k]] & 0xFFFu), P);
-      if (xp != xp) ni = min(ni, hid[k]);
-      else argmax_merge(bv, bi, xp, hid[k]);
+    // the window ids' penalised values (their raw logits fetched now)
+    for (int s = t; s < X.ns; s += WG) {
+      const uint32_t hw = X.hword[s];
+      if (hw == HW_EMPTY) continue;
+      const int id = (int)(hw >> 12);
+      const double xp = penalise(E::scalar(rowp, id), (int)(hw & 0xFFFu), P);
+      if (xp != xp) ni = min(ni, id);
+      else argmax_merge(bv, bi, xp, id);
     }
     block_argmax(bv, bi, red_d, red_i);
     ni = block_min(ni, red_i, INT_MAX);
@@ -875,27 +912,70 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
     const uint32_t th = kth_of_lanes(ck, pub_r);
     if (lane_id() == 0) lpub[wave_id()] = th;
   }
+  // the window ids this wave's threads own: raw logits (and penalised
+  // values, rounded to fp32 for the region test) into the index, the
+  // penalty corrections into the wave's record
+  {
+    double xpk[HPT];
+    double pm = -__builtin_inf();
+#pragma unroll
+    for (int k = 0; k < HPT; ++k) {
+      xpk[k] = 0.0;
+      if (hslot[k] < 0) continue;
+      xpk[k] = penalise(gval[k], (int)(X.hword[hslot[k]] & 0xFFFu), P);
+      X.hval[hslot[k]] = gval[k];
+      X.hpen[hslot[k]] = (float)xpk[k];
+      pm = (double)gval[k] > pm ? (double)gval[k] : pm;
+      pm = xpk[k] > pm ? xpk[k] : pm;
+    }
+    pm = wave_reduce(pm, OpMax());
+    // NaN / +-inf windows leave Rc at 0 (their rows go to the exact kernel)
+    const double Rc = (pm > -__builtin_inf() && pm < __builtin_inf()) ? ceil(pm * kc) : 0.0;
+    double corr = 0.0, pr = 0.0, pmx = -__builtin_inf();
+    int fl = 0;
+#pragma unroll
+    for (int k = 0; k < HPT; ++k) {
+      if (hslot[k] < 0) continue;
+      const double xp = xpk[k];
+      // fp32 terms (each <= 1) are within TOL_T of the exact ones
+      const double tr = (double)__builtin_amdgcn_exp2f((float)((double)gval[k] * kc - Rc));
+      const double tp = (double)__builtin_amdgcn_exp2f((float)(xp * kc - Rc));
+      pr += tr;
+      corr += tp - tr;
+      if (xp != xp) fl = 1;
+      else pmx = xp > pmx ? xp : pmx;
+    }
+    corr = wave_reduce(corr, OpAdd());
+    pr = wave_reduce(pr, OpAdd());
+    pmx = wave_reduce(pmx, OpMax());
+    fl = wave_reduce(fl, OpOr());
+    if (lane_id() == 0) {
+      s_pen[wave_id()].corr = corr;
+      s_pen[wave_id()].pr = pr;
+      s_pen[wave_id()].pmx = pmx;
+      s_pen[wave_id()].Rc = Rc;
+      s_pen[wave_id()].fl = fl;
+    }
+  }
   __syncthreads();
   if (krow <= 64) raise_tau(wb, kth_of_lanes(lds_load(lslots + lane_id()), krow));
   else if (pub_r > 0) raise_tau(wb, pub_min(lpub));
 
-  SState st{-__builtin_inff(), -__builtin_inff(), 0.0};
-  stream_stoch<BF16>(rs, q, nv, lo, pen_on, X, c, krow, pub_r, to_lds(&s_chunk), lslots, lpub,
-                     st, wb, ck);
-  if (s0 < hi) {
-    raise_tau(wb, lds_load(wb.shared));
-    stream_scalar<BF16>(rowp, s0, lo, hi, pen_on, X, c, true, st, wb, ck);
-  }
-
-  // ---- per wave, after its stream: (a) its region entries into the shared
-  // list, (b) the window ids its threads own -- raw terms out, penalised
-  // terms in, against the wave's own exponent offset Rc -- (c) its sums and
-  // state for the combination
+  SState st{-__builtin_inff(), 3.402823466e38f, -__builtin_inff(), 0.0};
   uint64_t* gk = (uint64_t*)(dyn + A.off_gather);
   int32_t* gi = (int32_t*)(dyn + A.off_gather + LEAN_CAP * 8);
   CX_LDS uint64_t* const lgk = to_lds(gk);
   CX_LDS int32_t* const lgi = to_lds(gi);
   CX_LDS int* const lcnt = to_lds(&s_cnt);
+  stream_stoch<BF16>(rs, q, qn, nv, lo, pen_on, X, c, krow, pub_r, to_lds(&s_chunk), lslots,
+                     lpub, st, wb, ck);
+  if (s0 < hi) {
+    raise_tau(wb, lds_load(wb.shared));
+    stream_scalar<BF16>(rowp, s0, lo, hi, pen_on, X, c, true, st, wb, ck);
+  }
+
+  // ---- per wave, after its stream: its region entries into the shared
+  // list, its sums and state for the combination
   raise_tau(wb, lds_load(wb.shared));
   {
     const int n = wb.n;
@@ -907,87 +987,71 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
       }
     }
   }
-  const float Rw = wave_reduce(st.R, OpMax());
-  double sl = st.s != 0.0 ? __builtin_ldexp(st.s, (int)fmaxf(st.R - Rw, -2048.0f)) : 0.0;
-  double corr = 0.0, pr = 0.0, pmx = -__builtin_inf();
-  int fl = st.s != st.s ? 1 : 0;
-  double Rc = -__builtin_inf();
   {
-    double pm = -__builtin_inf();
-    double xpk[HPT];
-#pragma unroll
-    for (int k = 0; k < HPT; ++k) {
-      xpk[k] = 0.0;
-      if (hslot[k] < 0) continue;
-      X.hval[hslot[k]] = gval[k];                      // for the general path
-      xpk[k] = penalise(gval[k], (int)(X.hword[hslot[k]] & 0xFFFu), P);
-      const double xr = (double)gval[k];
-      pm = xr > pm ? xr : pm;
-      pm = xpk[k] > pm ? xpk[k] : pm;
-    }
-    pm = wave_reduce(pm, OpMax());
-    // every correction term is at most 1; NaN / +-inf windows leave Rc at 0
-    // (their rows are resolved by the multi-pass kernel)
-    Rc = (pm > -__builtin_inf() && pm < __builtin_inf()) ? ceil(pm * kc) : 0.0;
-    const double thr_w = wb.tau <= 1u ? -__builtin_inf() : (double)key2f(wb.tau);
-#pragma unroll
-    for (int k = 0; k < HPT; ++k) {
-      if (hslot[k] < 0) continue;
-      const double xp = xpk[k];
-      const double tr = exp2((double)gval[k] * kc - Rc);
-      const double tp = exp2(xp * kc - Rc);
-      pr += tr;
-      corr += tp - tr;
-      if (xp != xp) {
-        fl = 1;
-      } else {
-        pmx = xp > pmx ? xp : pmx;
-        if (xp >= thr_w) {
-          const int pos = __hip_atomic_fetch_add(lcnt, 1, CX_RELAXED_WG);
-          if (pos < LEAN_CAP) { lgk[pos] = d2key(xp); lgi[pos] = hid[k]; }
-        }
+    // this wave's share of the window ids: penalised values at or above its
+    // threshold (fp32 pre-test, exact value for the survivors)
+    const int per = X.ns / NWAVE;
+    const float thr_f = wb.tauf;
+    const double thr_w = wb.tau <= 1u ? -__builtin_inf() : (double)wb.tauf;
+    for (int s = wave_id() * per + lane_id(); s < (wave_id() + 1) * per; s += 64) {
+      const uint32_t hw = X.hword[s];
+      if (hw == HW_EMPTY) continue;
+      // rounding is monotone: xp >= thr_f (a float) implies fp32(xp) >= thr_f
+      if (!(X.hpen[s] >= thr_f)) continue;
+      const double xp = penalise(X.hval[s], (int)(hw & 0xFFFu), P);
+      if (xp == xp && xp >= thr_w) {
+        const int pos = __hip_atomic_fetch_add(lcnt, 1, CX_RELAXED_WG);
+        if (pos < LEAN_CAP) { lgk[pos] = d2key(xp); lgi[pos] = (int32_t)(hw >> 12); }
       }
     }
   }
+  const float Rw = wave_reduce(st.R, OpMax());
+  double sl = st.s != 0.0 ? __builtin_ldexp(st.s, (int)fmaxf(st.R - Rw, -2048.0f)) : 0.0;
   sl = wave_reduce(sl, OpAdd());
-  corr = wave_reduce(corr, OpAdd());
-  pr = wave_reduce(pr, OpAdd());
-  pmx = wave_reduce(pmx, OpMax());
   const uint32_t kmx_w = wave_reduce(ck, OpMax());
-  fl = wave_reduce(fl, OpOr());
+  const int fl = wave_reduce(st.s != st.s ? 1 : 0, OpOr());
   if (krow <= 64) publish_top(ck, NSLOT, lslots + NSLOT * wave_id());
   if (lane_id() == 0) {
     w_s[wave_id()] = sl;
-    w_corr[wave_id()] = corr;
-    w_pr[wave_id()] = pr;
-    w_pmx[wave_id()] = pmx;
-    w_Rc[wave_id()] = Rc;
     w_R[wave_id()] = Rw;
     w_tau[wave_id()] = wb.tau;
     w_kmx[wave_id()] = kmx_w;
     w_fl[wave_id()] = fl | (wb.overflow ? 2 : 0);
   }
-  __syncthreads();
+  // Top-k rows the one-wave finish can take (static conditions): the last
+  // wave to get here decides the row, the others are done.
+  const bool lean_static = single && P.top_k > 0 && P.top_k <= 64 && P.typical_p >= 1.0 &&
+                           !A.out_probs && A.logV * (1.0 / P.temperature) <= 740.0;
+  if (lean_static) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    int arrived = 0;
+    if (lane_id() == 0) arrived = __hip_atomic_fetch_add(to_lds(&s_done), 1, __ATOMIC_ACQ_REL,
+                                                         __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (__builtin_amdgcn_readfirstlane(arrived) != NWAVE - 1) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  } else {
+    __syncthreads();
+  }
 
   // ---- combine: S = sum over waves of 2^(Rw - Rb) s_w + 2^(Rc_w - Rb) corr_w
   // (lane w of row 0 reads wave w's record)
   const int lw = lane_id() & 15;
   const float Rl = w_R[lw];
-  const double Rcl = w_Rc[lw];
+  const double Rcl = s_pen[lw].Rc;
   const float Rf = row0_reduce(Rl, OpMax());
   uint32_t Tf = row0_reduce(w_tau[lw], OpMax());
   const uint32_t kmx = row0_reduce(w_kmx[lw], OpMax());
-  const int flw = row0_reduce(w_fl[lw], OpOr());
+  const int flw = row0_reduce(w_fl[lw] | s_pen[lw].fl, OpOr());
   const int anynan = flw & 1, ovf = flw & 2;
   if (krow <= 64) Tf = max(Tf, kth_of_lanes(lds_load(lslots + lane_id()), krow));
-  const double PMX = row0_reduce(w_pmx[lw], OpMax());
+  const double PMX = row0_reduce(s_pen[lw].pmx, OpMax());
   const double Rb = fmax((double)Rf, row0_reduce(Rcl, OpMax()));
   // an exponent offset past +-2^22 leaves fp32 term arguments inexact
   const bool rb_ok = Rf > -__builtin_inff() && fabs(Rb) < 4194304.0;
   double Ss = 0.0, PR = 0.0;
   if (rb_ok) {
     const double sw = w_s[lw];
-    const double cw = w_corr[lw], pw = w_pr[lw];
+    const double cw = s_pen[lw].corr, pw = s_pen[lw].pr;
     const int dc = (int)fmax(Rcl - Rb, -2048.0);
     const double term = (sw != 0.0 ? __builtin_ldexp(sw, (int)fmax((double)Rl - Rb, -2048.0)) : 0.0) +
                         (cw != 0.0 ? __builtin_ldexp(cw, dc) : 0.0);
@@ -999,11 +1063,14 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   const bool sum_ok = !anynan && rb_ok && Ss > 0.0 && Ss < __builtin_inf() && tol <= TOL_MAX;
   const int nlist = s_cnt;
 
-  // ---- lean finish (one slice, top-k <= 64, short list, nothing exotic):
-  // wave 0 decides; a row it cannot decide is left pending for the exact path
-  if (single && sum_ok && !ovf && P.top_k > 0 && P.top_k <= 64 && P.typical_p >= 1.0 &&
-      !A.out_probs && A.logV * invT <= 740.0 && nlist <= LEAN_CAP) {
-    if (wave_id() != 0) return;
+  // ---- lean finish: this wave decides; a row it cannot decide (inexact
+  // sum, tie flood, long list, near a top-p boundary) is left pending for
+  // the exact kernel
+  if (lean_static) {
+    if (!(sum_ok && !ovf && nlist <= LEAN_CAP)) {
+      if (lane_id() == 0) { A.out_id[row] = -1; A.row_status[row] = ROW_PENDING; }
+      return;
+    }
     const uint64_t thr64 = Tf <= 1u ? 1ull : d2key((double)key2f(Tf));
     int tok = -1;
     const bool ok = lean_decide(A, row, P, lgk, lgi, nlist, thr64, kc, Rb, Ss, tol,
