@@ -8,10 +8,12 @@ already resident in HBM.  A step is one cx_sample_f32 call over the batch.
 
   value        sampled rows/s over exactly `--steps` timed steps
   roofline     algorithmic bytes of one launch / the fused kernel's mean
-               duration (hipEvent pairs the library records around each
-               launch on its own stream), against 8 TB/s
+               duration (start / stop events the dispatch itself records,
+               on the kernel's stream), against 8 TB/s; traffic from the
+               FETCH_SIZE / WRITE_SIZE summary in profiles/
   cpu_baseline the NumPy oracle on the host, one core, on a bounded sample
-               of the same rows (reported beside, not a target)
+               of the same rows (reported beside, not a target); also a
+               process pool of up to 16 workers (cpu_baseline_pool)
 
 The other workloads (nucleus, speculative verify, heterogeneous bf16) are
 timed the same way and reported under "other_workloads".
@@ -136,6 +138,42 @@ def cpu_baseline(w, seconds: float) -> dict:
                       f"{np.__version__}, single thread, {_cpu_model()})"}
 
 
+_POOL_W = None
+
+
+def _pool_init(w):
+    global _POOL_W
+    _POOL_W = w
+
+
+def _pool_rows(args):
+    """Rows [lo, hi) of the pool workload through the oracle; returns the count."""
+    from oracle import sampler_ref as R
+    lo, hi = args
+    w = _POOL_W
+    hl = R.hist_rows_to_lists(w.hist, w.hist_len) if w.hist.size else None
+    for i in range(lo, hi):
+        b = i % w.B
+        R.sample_row(w.logits[b], w.params[b], None if hl is None else hl[b], float(w.u[b]))
+    return hi - lo
+
+
+def cpu_baseline_pool(w, rows_per_worker: int, workers: int) -> dict:
+    """The same oracle in a process pool, `workers` processes (one core each),
+    `rows_per_worker` rows each: the multi-core CPU figure."""
+    import multiprocessing as mp
+    ctx = mp.get_context("fork")
+    with ctx.Pool(workers, initializer=_pool_init, initargs=(w,)) as pool:
+        pool.map(_pool_rows, [(0, 1)] * workers)            # warm the workers
+        t0 = time.perf_counter()
+        n = sum(pool.map(_pool_rows, [(k * rows_per_worker, (k + 1) * rows_per_worker)
+                                      for k in range(workers)]))
+        dt = time.perf_counter() - t0
+    return {"value": round(n / dt, 2), "unit": "rows/s", "cores": workers, "kind": "port",
+            "sample": f"{n} rows of the B={w.B} V={w.V} workload in a {workers}-process pool "
+                      f"({dt:.1f} s, numpy {np.__version__}, {_cpu_model()})"}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -154,16 +192,30 @@ def main() -> int:
               file=sys.stderr)
         return 2
 
+    from chenxing_amd import workloads as W
+    _say("[bench] generating full_penalty workload")
+    w = W.full_penalty()
+
+    # The CPU figures come first: the process pool forks before this process
+    # touches the GPU.
+    cpu = cpu_pool = None
+    if args.cpu_seconds > 0:
+        _say("[bench] CPU baseline (oracle)")
+        cpu = cpu_baseline(w, args.cpu_seconds)
+        # the pool: as many rows per worker as one core did in about half
+        # the single-core time, on at most 16 workers
+        workers = max(1, min(16, os.cpu_count() or 1))
+        per = max(4, int(cpu["value"] * args.cpu_seconds / 2))
+        _say(f"[bench] CPU baseline, {workers}-process pool")
+        cpu_pool = cpu_baseline_pool(w, per, workers)
+
     import torch
-    from chenxing_amd import _lib, workloads as W
+    from chenxing_amd import _lib
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         return 1
     _lib.load()
     dev = torch.device("cuda:0")
-
-    _say("[bench] generating full_penalty workload")
-    w = W.full_penalty()
     ds = DeviceSample(w, dev)
     _say("[bench] timing full_penalty")
     step_ms, kern_ms = time_steps(ds, args.steps, args.warmup, _lib.KERNEL_SAMPLE)
@@ -215,11 +267,6 @@ def main() -> int:
         del src, dst
         torch.cuda.empty_cache()
 
-    cpu = None
-    if args.cpu_seconds > 0:
-        _say("[bench] CPU baseline (oracle)")
-        cpu = cpu_baseline(w, args.cpu_seconds)
-
     out = {
         "metric": METRIC,
         "value": round(rows_per_s, 1),
@@ -242,6 +289,7 @@ def main() -> int:
                      "traffic": None, "kernel": "cx::sample_kernel<false>",
                      "kernel_ms": round(kern_ms, 5), "algorithmic_bytes": nbytes},
         "cpu_baseline": cpu,
+        "cpu_baseline_pool": cpu_pool,
         "row_outcomes": outcomes,
         "other_workloads": other,
     }

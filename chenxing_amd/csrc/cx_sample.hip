@@ -1162,13 +1162,12 @@ int launch_sample(const SampleArgs& A, hipStream_t s) {
     if (e != hipSuccess) return (int)e;
     attr_set[A.bf16] = A.lds_bytes;
   }
-  {
-    TimedScope ts(CX_KERNEL_SAMPLE, s);
-    if (A.bf16)
-      hipLaunchKernelGGL(sample_kernel<true>, dim3(A.B * A.nsplit), dim3(WG), A.lds_bytes, s, A);
-    else
-      hipLaunchKernelGGL(sample_kernel<false>, dim3(A.B * A.nsplit), dim3(WG), A.lds_bytes, s, A);
-  }
+  if (A.bf16)
+    timed_launch(CX_KERNEL_SAMPLE, sample_kernel<true>, dim3(A.B * A.nsplit), dim3(WG),
+                 A.lds_bytes, s, A);
+  else
+    timed_launch(CX_KERNEL_SAMPLE, sample_kernel<false>, dim3(A.B * A.nsplit), dim3(WG),
+                 A.lds_bytes, s, A);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || A.nsplit == 1) return (int)e;
   static int fin_attr = 0;
@@ -1178,8 +1177,7 @@ int launch_sample(const SampleArgs& A, hipStream_t s) {
     if (e != hipSuccess) return (int)e;
     fin_attr = A.fin_lds_bytes;
   }
-  TimedScope tf(CX_KERNEL_SAMPLE_FINISH, s);
-  hipLaunchKernelGGL(finish_kernel, dim3(A.B), dim3(WG), A.fin_lds_bytes, s, A);
+  timed_launch(CX_KERNEL_SAMPLE_FINISH, finish_kernel, dim3(A.B), dim3(WG), A.fin_lds_bytes, s, A);
   return (int)hipGetLastError();
 }
 }  // namespace cx

@@ -40,9 +40,8 @@ int launch_slow(const SampleArgs& A, hipStream_t s) {
     if (e != hipSuccess) return (int)e;
     attr = A.slow_lds_bytes;
   }
-  TimedScope ts(CX_KERNEL_SAMPLE_SLOW, s);
   const int grid = (A.B + SLOW_ROWS_PER_WG - 1) / SLOW_ROWS_PER_WG;
-  hipLaunchKernelGGL(slow_kernel, dim3(grid), dim3(WG), A.slow_lds_bytes, s, A);
+  timed_launch(CX_KERNEL_SAMPLE_SLOW, slow_kernel, dim3(grid), dim3(WG), A.slow_lds_bytes, s, A);
   return (int)hipGetLastError();
 }
 

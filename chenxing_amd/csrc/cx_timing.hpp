@@ -1,6 +1,11 @@
-// cx_timing.hpp -- opt-in hipEvent timing around library kernel launches.
+// cx_timing.hpp -- opt-in per-launch kernel timing.  While timing is on,
+// every library kernel is launched with hipExtLaunchKernelGGL and a start /
+// stop event pair that the dispatch itself records (the kernel's own
+// execution interval on its stream, not the host's launch overhead).
 #pragma once
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
+#include <stdint.h>
 #include <mutex>
 #include <vector>
 
@@ -30,26 +35,27 @@ struct Timing {
 
 Timing& timing();
 
-// Brackets one kernel launch with events on its stream when timing is on.
-struct TimedScope {
-  int kind;
-  hipStream_t s;
-  hipEvent_t a = nullptr, b = nullptr;
-  TimedScope(int k, hipStream_t st) : kind(k), s(st) {
-    Timing& T = timing();
-    if (!T.on) return;
-    std::lock_guard<std::mutex> g(T.mu);
-    a = T.take();
-    b = T.take();
-    if (a) (void)hipEventRecord(a, s);
+// Launch `kernel`; with timing on, its execution interval is recorded under
+// `kind` (one of the CX_KERNEL_* ids).
+template <typename F, typename... Args>
+inline void timed_launch(int kind, F kernel, dim3 grid, dim3 block, uint32_t lds, hipStream_t s,
+                         Args... args) {
+  Timing& T = timing();
+  if (T.on) {
+    hipEvent_t a = nullptr, b = nullptr;
+    {
+      std::lock_guard<std::mutex> g(T.mu);
+      a = T.take();
+      b = T.take();
+    }
+    if (a && b) {
+      hipExtLaunchKernelGGL(kernel, grid, block, lds, s, a, b, 0u, args...);
+      std::lock_guard<std::mutex> g(T.mu);
+      T.rec[kind].push_back({a, b});
+      return;
+    }
   }
-  ~TimedScope() {
-    if (!a || !b) return;
-    (void)hipEventRecord(b, s);
-    Timing& T = timing();
-    std::lock_guard<std::mutex> g(T.mu);
-    T.rec[kind].push_back({a, b});
-  }
-};
+  hipLaunchKernelGGL(kernel, grid, block, lds, s, args...);
+}
 
 }  // namespace cx

@@ -410,15 +410,11 @@ __global__ __launch_bounds__(WG) void verify_draw(VerifyArgs A) {
 int launch_verify(const VerifyArgs& A, bool any_stochastic, hipStream_t s) {
   const int nt = A.B * (A.gamma + 1);
   const int nrows = nt + (any_stochastic ? A.B * A.gamma : 0);
-  {
-    TimedScope ts(CX_KERNEL_VERIFY_STATS, s);
-    hipLaunchKernelGGL(verify_stats, dim3(nrows * A.nchunk), dim3(WG), 0, s, A);
-  }
-  TimedScope ts(CX_KERNEL_VERIFY_REST, s);
-  hipLaunchKernelGGL(verify_decide, dim3(A.B), dim3(WG), 0, s, A);
+  timed_launch(CX_KERNEL_VERIFY_STATS, verify_stats, dim3(nrows * A.nchunk), dim3(WG), 0, s, A);
+  timed_launch(CX_KERNEL_VERIFY_REST, verify_decide, dim3(A.B), dim3(WG), 0, s, A);
   if (any_stochastic) {
-    hipLaunchKernelGGL(verify_residual, dim3(A.B * A.nchunk), dim3(WG), 0, s, A);
-    hipLaunchKernelGGL(verify_draw, dim3(A.B), dim3(WG), 0, s, A);
+    timed_launch(CX_KERNEL_VERIFY_REST, verify_residual, dim3(A.B * A.nchunk), dim3(WG), 0, s, A);
+    timed_launch(CX_KERNEL_VERIFY_REST, verify_draw, dim3(A.B), dim3(WG), 0, s, A);
   }
   return (int)hipGetLastError();
 }

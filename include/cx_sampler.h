@@ -134,12 +134,13 @@ int cx_spec_verify_host(const float* target, const float* draft, const int32_t* 
                         int32_t* accepted, int32_t* next_tok, int32_t* used,
                         int32_t* row_status);
 
-/* Kernel timing (measurement only).  While enabled, the library records a
- * hipEvent pair around every launch of the selected kernels, on the stream
- * the kernel is launched on.  cx_timing_read waits for the recorded events,
- * returns the summed milliseconds and launch count of one kernel and
- * forgets its records.  No counterpart in the reference (which has no
- * device code); callers are benchmarks and profilers. */
+/* Kernel timing (measurement only).  While enabled, every library kernel is
+ * dispatched with a start / stop event pair recorded by the dispatch itself
+ * (hipExtLaunchKernel): the kernel's execution interval on its stream.
+ * cx_timing_read waits for the recorded events, returns the summed
+ * milliseconds and launch count of one kernel kind and forgets its records.
+ * No counterpart in the reference (which has no device code); callers are
+ * benchmarks and profilers. */
 #define CX_KERNEL_SAMPLE        0  /* fused sampler kernel            */
 #define CX_KERNEL_SAMPLE_SLOW   1  /* exact multi-pass row kernel     */
 #define CX_KERNEL_VERIFY_STATS  2  /* verify: stats over all rows     */
