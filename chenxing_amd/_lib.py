@@ -30,7 +30,16 @@ _SIGS = {
                                 _P, _P, _P, _P, C.c_size_t, _P]),
     "cx_sample_bf16": (C.c_int, [_P, C.c_int64, C.c_int32, C.c_int32, _P, _P, C.c_int64, _P, _P,
                                  _P, _P, _P, _P, C.c_size_t, _P]),
+    "cx_sample_f64": (C.c_int, [_P, C.c_int64, C.c_int32, C.c_int32, _P, _P, C.c_int64, _P, _P,
+                                _P, _P, _P, _P, C.c_size_t, _P]),
     "cx_sample_workspace_bytes": (C.c_size_t, [C.c_int32, C.c_int32, C.c_int64]),
+    "cx_apply_penalties": (C.c_int, [_P, C.c_int32, C.c_int64, C.c_int32, C.c_int32, _P, _P,
+                                     C.c_int64, _P, _P, C.c_int64, _P, _P]),
+    "cx_apply_penalties_host": (C.c_int, [_P, C.c_int32, C.c_int64, C.c_int32, C.c_int32, _P,
+                                          _P, C.c_int64, _P, _P, _P]),
+    "cx_truncate_f64": (C.c_int, [_P, C.c_int64, C.c_int32, C.c_int32, _P, _P, C.c_int64, _P,
+                                  _P]),
+    "cx_truncate_host": (C.c_int, [_P, C.c_int64, C.c_int32, C.c_int32, _P, _P, _P]),
     "cx_sample_host": (C.c_int, [_P, C.c_int32, C.c_int64, C.c_int32, C.c_int32, _P, _P,
                                  C.c_int64, _P, _P, _P, _P, _P]),
     "cx_spec_verify_f32": (C.c_int, [_P, _P, _P, _P, _P, C.c_int32, C.c_int32, C.c_int32, _P, _P,
@@ -98,29 +107,76 @@ def _prep_hist(hist, hist_len, B):
     return h, hl, h.shape[1]
 
 
-def sample_host(logits: np.ndarray, params, hist=None, hist_len=None, u=None,
-                bf16: bool = False, want_probs: bool = False):
-    """Numpy in / numpy out: (ids [B], status [B], probs [B, V] or None).
-
-    ``logits`` is [B, V] float32, or uint16 bf16 bit patterns with ``bf16=True``.
-    """
-    lib = load()
-    x = np.ascontiguousarray(logits, dtype=np.uint16 if bf16 else np.float32)
-    if x.ndim != 2:
-        raise ValueError("logits must be [B, V]")
-    B, V = x.shape
+def _prep_params(params, B):
     prm = params if isinstance(params, np.ndarray) and params.dtype == ROW_DTYPE \
         else pack_rows(params if isinstance(params, (list, tuple)) else [params] * B)
     if prm.shape[0] != B:
         raise ValueError("need one parameter row per logits row")
+    return np.ascontiguousarray(prm)
+
+
+def _logits_dtype(logits, bf16: bool):
+    """(contiguous array, dtype code): fp32 = 0, bf16 bits = 1, fp64 = 2."""
+    if bf16:
+        return np.ascontiguousarray(logits, dtype=np.uint16), 1
+    a = np.asarray(logits)
+    if a.dtype == np.float64:
+        return np.ascontiguousarray(a), 2
+    return np.ascontiguousarray(a, dtype=np.float32), 0
+
+
+def sample_host(logits: np.ndarray, params, hist=None, hist_len=None, u=None,
+                bf16: bool = False, want_probs: bool = False):
+    """Numpy in / numpy out: (ids [B], status [B], probs [B, V] or None).
+
+    ``logits`` is [B, V] float32 or float64 (float64 rows take the exact
+    multi-pass path), or uint16 bf16 bit patterns with ``bf16=True``.
+    """
+    lib = load()
+    x, code = _logits_dtype(logits, bf16)
+    if x.ndim != 2:
+        raise ValueError("logits must be [B, V]")
+    B, V = x.shape
+    prm = _prep_params(params, B)
     uu = np.zeros(B) if u is None else np.ascontiguousarray(u, dtype=np.float64)
     h, hl, ldh = _prep_hist(hist, hist_len, B)
     ids = np.empty(B, np.int32)
     st = np.empty(B, np.int32)
     probs = np.empty((B, V), np.float32) if want_probs else None
-    _check(lib.cx_sample_host(_ptr(x), 1 if bf16 else 0, V, B, V, _ptr(h), _ptr(hl), ldh,
+    _check(lib.cx_sample_host(_ptr(x), code, V, B, V, _ptr(h), _ptr(hl), ldh,
                               _ptr(prm), _ptr(uu), _ptr(ids), _ptr(st), _ptr(probs)))
     return ids, st, probs
+
+
+def apply_penalties_host(logits: np.ndarray, params, hist=None, hist_len=None,
+                         bf16: bool = False):
+    """[B, V] logits (fp32, fp64 or bf16 bits) -> (fp64 [B, V], status [B])."""
+    lib = load()
+    x, code = _logits_dtype(logits, bf16)
+    if x.ndim != 2:
+        raise ValueError("logits must be [B, V]")
+    B, V = x.shape
+    prm = _prep_params(params, B)
+    h, hl, ldh = _prep_hist(hist, hist_len, B)
+    out = np.empty((B, V), np.float64)
+    st = np.empty(B, np.int32)
+    _check(lib.cx_apply_penalties_host(_ptr(x), code, V, B, V, _ptr(h), _ptr(hl), ldh,
+                                       _ptr(prm), _ptr(out), _ptr(st)))
+    return out, st
+
+
+def truncate_host(probs: np.ndarray, params):
+    """[B, V] fp64 probabilities -> (filtered fp64 [B, V], status [B])."""
+    lib = load()
+    p = np.ascontiguousarray(probs, dtype=np.float64)
+    if p.ndim != 2:
+        raise ValueError("probs must be [B, V]")
+    B, V = p.shape
+    prm = _prep_params(params, B)
+    out = np.empty((B, V), np.float64)
+    st = np.empty(B, np.int32)
+    _check(lib.cx_truncate_host(_ptr(p), V, B, V, _ptr(prm), _ptr(out), _ptr(st)))
+    return out, st
 
 
 def spec_verify_host(target: np.ndarray, draft: np.ndarray | None, draft_ids: np.ndarray,
@@ -189,9 +245,11 @@ def sample_device(logits, prm, u, hist=None, hist_len=None, out_id=None, row_sta
     ldh = 0 if hist is None else hist.shape[1]
     nbytes = lib.cx_sample_workspace_bytes(B, V, ldh)
     ws = _ws_sample.get(nbytes, dev)
-    fn = lib.cx_sample_bf16 if logits.dtype == torch.bfloat16 else lib.cx_sample_f32
-    if logits.dtype not in (torch.bfloat16, torch.float32):
-        raise ValueError("logits must be float32 or bfloat16")
+    fns = {torch.bfloat16: lib.cx_sample_bf16, torch.float32: lib.cx_sample_f32,
+           torch.float64: lib.cx_sample_f64}
+    if logits.dtype not in fns:
+        raise ValueError("logits must be float32, bfloat16 or float64")
+    fn = fns[logits.dtype]
     _check(fn(_P(logits.data_ptr()), logits.stride(0), B, V,
               _P(hist.data_ptr()) if hist is not None else None,
               _P(hist_len.data_ptr()) if hist_len is not None else None, ldh,
@@ -230,7 +288,8 @@ def header_symbols() -> list[str]:
                                  flags=re.M)))
 
 
-KERNEL_SAMPLE, KERNEL_SAMPLE_SLOW, KERNEL_VERIFY_STATS, KERNEL_VERIFY_REST, KERNEL_SAMPLE_FINISH = 0, 1, 2, 3, 4
+(KERNEL_SAMPLE, KERNEL_SAMPLE_SLOW, KERNEL_VERIFY_STATS, KERNEL_VERIFY_REST,
+ KERNEL_SAMPLE_FINISH, KERNEL_PENALTIES, KERNEL_TRUNCATE) = range(7)
 
 
 def timing_enable(on: bool = True) -> None:

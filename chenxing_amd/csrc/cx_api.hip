@@ -14,6 +14,8 @@
 namespace cx {
 int launch_sample(const SampleArgs& A, hipStream_t s);
 int launch_slow(const SampleArgs& A, hipStream_t s);
+int launch_penalties(const SampleArgs& A, hipStream_t s);
+int launch_truncate(const SampleArgs& A, hipStream_t s);
 int launch_verify(const VerifyArgs& A, bool any_stochastic, hipStream_t s);
 
 static thread_local std::string g_err;
@@ -48,7 +50,30 @@ static int ilog2(int x) {
   return l;
 }
 
-static int sample_impl(const void* logits, int bf16, int64_t ld, int32_t B, int32_t V,
+// Penalty hash size and the dynamic LDS layout of the exact multi-pass row
+// path: full-row bitmap, hash keys, histogram / gather work area and
+// per-thread sums.
+static void slow_layout(SampleArgs& A, int32_t V, int64_t ldh) {
+  const long win = ldh > 0 ? (ldh < WIN_MAX ? ldh : WIN_MAX) : 0;   // window capacity
+  if (ldh > 0) {
+    A.ns = pow2_at_least(2 * win > 64 ? 2 * win : 64);
+    A.ns_log2 = ilog2(A.ns);
+  }
+  long bits = ldh > 0 ? pow2_at_least(V) : 32;
+  if (bits > (1 << 18)) bits = 1 << 18;
+  A.slow_nbw = (int)(bits / 32 > 1 ? bits / 32 : 1);
+  size_t so = align_up((size_t)A.slow_nbw * 4, 16);
+  A.slow_off_hkey = (int)so;
+  so = align_up(so + (size_t)A.ns * 4, 16);
+  A.slow_off_work = (int)so;
+  so = align_up(so + 1024 * 12 + 1024 * 24, 16);
+  A.slow_off_tsum = (int)so;
+  so += (size_t)WG * 8;
+  A.slow_lds_bytes = (int)so;
+}
+
+// dtype: 0 fp32, 1 bf16, 2 fp64 (every row on the exact multi-pass path).
+static int sample_impl(const void* logits, int dtype, int64_t ld, int32_t B, int32_t V,
                        const int32_t* hist, const int32_t* hist_len, int64_t ldh,
                        const cx_row_params* prm, const double* u, int32_t* out_id,
                        int32_t* row_status, float* out_probs, void* ws, size_t ws_bytes,
@@ -87,15 +112,13 @@ static int sample_impl(const void* logits, int bf16, int64_t ld, int32_t B, int3
   A.nsplit = choose_nsplit(B, V);
   int per = (V + A.nsplit - 1) / A.nsplit;
   A.split_len = (per + 7) / 8 * 8;
-  A.bf16 = bf16;
+  A.bf16 = dtype == 1;
+  A.f64 = dtype == 2;
+  A.all_slow = dtype == 2;
   A.logV = log((double)V);
-  const int esz = bf16 ? 2 : 4;
+  const int esz = dtype == 2 ? 8 : (dtype == 1 ? 2 : 4);
   A.vec_ok = (((uintptr_t)logits) % 16 == 0) && ((ld * esz) % 16 == 0);
-  const long win = ldh > 0 ? (ldh < WIN_MAX ? ldh : WIN_MAX) : 0;   // window capacity
-  if (ldh > 0) {
-    A.ns = pow2_at_least(2 * win > 64 ? 2 * win : 64);
-    A.ns_log2 = ilog2(A.ns);
-  }
+  slow_layout(A, V, ldh);
   // fused kernel: penalty index (bitmap of the slice's window ids, hash of
   // (id << 12 | count) words and the ids' raw logits) and the per-wave
   // candidate buffers
@@ -117,31 +140,56 @@ static int sample_impl(const void* logits, int bf16, int64_t ld, int32_t B, int3
   A.off_gather = (int)off;
   off += (size_t)LEAN_CAP * 12;
   size_t fin = (size_t)SORT_CAP * (8 + 4 + 4 + 8 + 8);
-  {  // multi-pass row path: full-row bitmap + hash keys + histogram / gather
-     // work area + per-thread sums; shares the dynamic LDS of the kernel
-     // that runs it
-    long bits = ldh > 0 ? pow2_at_least(V) : 32;
-    if (bits > (1 << 18)) bits = 1 << 18;
-    A.slow_nbw = (int)(bits / 32 > 1 ? bits / 32 : 1);
-    size_t so = align_up((size_t)A.slow_nbw * 4, 16);
-    A.slow_off_hkey = (int)so;
-    so = align_up(so + (size_t)A.ns * 4, 16);
-    A.slow_off_work = (int)so;
-    so = align_up(so + 1024 * 12 + 1024 * 24, 16);
-    A.slow_off_tsum = (int)so;
-    so += (size_t)WG * 8;
-    A.slow_lds_bytes = (int)so;
-    if (so > fin) fin = so;
-    if (so > off) off = so;
-  }
+  const size_t so = (size_t)A.slow_lds_bytes;
+  if (so > fin) fin = so;
+  if (so > off) off = so;
   A.fin_lds_bytes = (int)fin;
   A.lds_bytes = (int)(A.nsplit > 1 ? off : (off > fin ? off : fin));
   if (A.lds_bytes > 150 * 1024) return fail(CX_EINVAL, "LDS layout too large (%d)", A.lds_bytes);
   hipStream_t s = (hipStream_t)stream;
-  int e = launch_sample(A, s);
-  if (e != 0) return hip_fail((hipError_t)e, "sample launch");
+  int e = 0;
+  if (!A.all_slow) {
+    e = launch_sample(A, s);
+    if (e != 0) return hip_fail((hipError_t)e, "sample launch");
+  }
   e = launch_slow(A, s);
   if (e != 0) return hip_fail((hipError_t)e, "slow-path launch");
+  return CX_OK;
+}
+
+// Sampler.apply_penalties / Sampler._truncate for a batch of rows.
+static int rowop_impl(bool trunc, const void* x, int dtype, int64_t ld, int32_t B, int32_t V,
+                      const int32_t* hist, const int32_t* hist_len, int64_t ldh,
+                      const cx_row_params* prm, double* out, int64_t ldo, int32_t* row_status,
+                      void* stream) {
+  g_err.clear();
+  if (dtype < 0 || dtype > 2) return fail(CX_EINVAL, "dtype must be 0 (fp32), 1 (bf16) or 2 (fp64)");
+  if (B < 0 || V < 1 || ld < V || ldo < V || ldh < 0)
+    return fail(CX_EINVAL, "bad shape: B=%d V=%d ld=%lld ldo=%lld ldh=%lld", B, V, (long long)ld,
+                (long long)ldo, (long long)ldh);
+  if (V >= (1 << 20)) return fail(CX_EINVAL, "V=%d exceeds the 2^20 token-id limit", V);
+  if (B == 0) return CX_OK;
+  if (!x || !prm || !out || !row_status) return fail(CX_EINVAL, "null pointer argument");
+  if (ldh > 0 && (!hist || !hist_len)) return fail(CX_EINVAL, "history pointers are null");
+  SampleArgs A;
+  memset(&A, 0, sizeof A);
+  A.logits = x;
+  A.ld = ld;
+  A.B = B;
+  A.V = V;
+  A.hist = hist;
+  A.hist_len = hist_len;
+  A.ldh = trunc ? 0 : ldh;
+  A.prm = prm;
+  A.row_status = row_status;
+  A.bf16 = dtype == 1;
+  A.f64 = dtype == 2;
+  A.out64 = out;
+  A.ldo = ldo;
+  slow_layout(A, V, A.ldh);
+  hipStream_t s = (hipStream_t)stream;
+  int e = trunc ? launch_truncate(A, s) : launch_penalties(A, s);
+  if (e != 0) return hip_fail((hipError_t)e, trunc ? "truncate launch" : "penalties launch");
   return CX_OK;
 }
 
@@ -214,6 +262,15 @@ int cx_sample_bf16(const uint16_t* logits, int64_t ld, int32_t B, int32_t V,
                      out_probs, workspace, ws_bytes, stream);
 }
 
+int cx_sample_f64(const double* logits, int64_t ld, int32_t B, int32_t V,
+                  const int32_t* hist, const int32_t* hist_len, int64_t ldh,
+                  const cx_row_params* prm, const double* u, int32_t* out_id,
+                  int32_t* row_status, float* out_probs, void* workspace, size_t ws_bytes,
+                  void* stream) {
+  return sample_impl(logits, 2, ld, B, V, hist, hist_len, ldh, prm, u, out_id, row_status,
+                     out_probs, workspace, ws_bytes, stream);
+}
+
 size_t cx_sample_workspace_bytes(int32_t B, int32_t V, int64_t ldh) {
   (void)ldh;
   if (B <= 0 || V <= 0) return 256;
@@ -225,10 +282,10 @@ int cx_sample_host(const void* logits, int32_t dtype, int64_t ld, int32_t B, int
                    const cx_row_params* prm, const double* u, int32_t* out_id,
                    int32_t* row_status, float* out_probs) {
   g_err.clear();
-  if (dtype != 0 && dtype != 1) return fail(CX_EINVAL, "dtype must be 0 (fp32) or 1 (bf16)");
+  if (dtype < 0 || dtype > 2) return fail(CX_EINVAL, "dtype must be 0 (fp32), 1 (bf16) or 2 (fp64)");
   if (B < 0 || V < 1 || ld < V || ldh < 0) return fail(CX_EINVAL, "bad shape");
   if (B == 0) return CX_OK;
-  const size_t esz = dtype ? 2 : 4;
+  const size_t esz = dtype == 2 ? 8 : (dtype == 1 ? 2 : 4);
   DevBuf dl, dh, dhl, dp, du, did, dst, dpr, dws;
   hipError_t e;
   const size_t ws = cx_sample_workspace_bytes(B, V, ldh);
@@ -259,6 +316,67 @@ int cx_sample_host(const void* logits, int32_t dtype, int64_t ld, int32_t B, int
       (e = hipMemcpy(out_probs, dpr.p, (size_t)B * V * 4, hipMemcpyDeviceToHost)))
     return hip_fail(e, "hipMemcpy");
   return CX_OK;
+}
+
+int cx_apply_penalties(const void* logits, int32_t dtype, int64_t ld, int32_t B, int32_t V,
+                       const int32_t* hist, const int32_t* hist_len, int64_t ldh,
+                       const cx_row_params* prm, double* out, int64_t ldo, int32_t* row_status,
+                       void* stream) {
+  return rowop_impl(false, logits, dtype, ld, B, V, hist, hist_len, ldh, prm, out, ldo,
+                    row_status, stream);
+}
+
+int cx_truncate_f64(const double* probs, int64_t ld, int32_t B, int32_t V,
+                    const cx_row_params* prm, double* out, int64_t ldo, int32_t* row_status,
+                    void* stream) {
+  return rowop_impl(true, probs, 2, ld, B, V, nullptr, nullptr, 0, prm, out, ldo, row_status,
+                    stream);
+}
+
+// Host-memory variant of both row operations.
+static int rowop_host(bool trunc, const void* x, int32_t dtype, int64_t ld, int32_t B, int32_t V,
+                      const int32_t* hist, const int32_t* hist_len, int64_t ldh,
+                      const cx_row_params* prm, double* out, int32_t* row_status) {
+  g_err.clear();
+  if (dtype < 0 || dtype > 2) return fail(CX_EINVAL, "dtype must be 0 (fp32), 1 (bf16) or 2 (fp64)");
+  if (B < 0 || V < 1 || ld < V || ldh < 0) return fail(CX_EINVAL, "bad shape");
+  if (B == 0) return CX_OK;
+  if (!x || !prm || !out || !row_status) return fail(CX_EINVAL, "null pointer argument");
+  if (ldh > 0 && (!hist || !hist_len)) return fail(CX_EINVAL, "history pointers are null");
+  const size_t esz = dtype == 2 ? 8 : (dtype == 1 ? 2 : 4);
+  DevBuf dx, dh, dhl, dp, dout, dst;
+  hipError_t e;
+  if ((e = dx.alloc((size_t)B * ld * esz)) || (e = dp.alloc(sizeof(cx_row_params) * B)) ||
+      (e = dout.alloc((size_t)B * V * 8)) || (e = dst.alloc(4 * (size_t)B)))
+    return hip_fail(e, "hipMalloc");
+  if (ldh > 0 && ((e = dh.alloc((size_t)B * ldh * 4)) || (e = dhl.alloc(4 * (size_t)B))))
+    return hip_fail(e, "hipMalloc");
+  if ((e = hipMemcpy(dx.p, x, (size_t)B * ld * esz, hipMemcpyHostToDevice)) ||
+      (e = hipMemcpy(dp.p, prm, sizeof(cx_row_params) * B, hipMemcpyHostToDevice)))
+    return hip_fail(e, "hipMemcpy");
+  if (ldh > 0 && ((e = hipMemcpy(dh.p, hist, (size_t)B * ldh * 4, hipMemcpyHostToDevice)) ||
+                  (e = hipMemcpy(dhl.p, hist_len, 4 * (size_t)B, hipMemcpyHostToDevice))))
+    return hip_fail(e, "hipMemcpy");
+  int rc = rowop_impl(trunc, dx.p, dtype, ld, B, V, (const int32_t*)dh.p, (const int32_t*)dhl.p,
+                      ldh, (const cx_row_params*)dp.p, (double*)dout.p, V, (int32_t*)dst.p,
+                      nullptr);
+  if (rc != CX_OK) return rc;
+  if ((e = hipDeviceSynchronize())) return hip_fail(e, trunc ? "truncate kernel" : "penalties kernel");
+  if ((e = hipMemcpy(out, dout.p, (size_t)B * V * 8, hipMemcpyDeviceToHost)) ||
+      (e = hipMemcpy(row_status, dst.p, 4 * (size_t)B, hipMemcpyDeviceToHost)))
+    return hip_fail(e, "hipMemcpy");
+  return CX_OK;
+}
+
+int cx_apply_penalties_host(const void* logits, int32_t dtype, int64_t ld, int32_t B, int32_t V,
+                            const int32_t* hist, const int32_t* hist_len, int64_t ldh,
+                            const cx_row_params* prm, double* out, int32_t* row_status) {
+  return rowop_host(false, logits, dtype, ld, B, V, hist, hist_len, ldh, prm, out, row_status);
+}
+
+int cx_truncate_host(const double* probs, int64_t ld, int32_t B, int32_t V,
+                     const cx_row_params* prm, double* out, int32_t* row_status) {
+  return rowop_host(true, probs, 2, ld, B, V, nullptr, nullptr, 0, prm, out, row_status);
 }
 
 int cx_spec_verify_f32(const float* target, const float* draft, const int32_t* draft_ids,
@@ -326,7 +444,8 @@ int cx_timing_enable(int on) {
 
 int cx_timing_read(int32_t kernel, double* total_ms, int64_t* launches) {
   g_err.clear();
-  if (kernel < 0 || kernel > 4 || !total_ms || !launches) return fail(CX_EINVAL, "bad timing query");
+  if (kernel < 0 || kernel >= CX_KERNEL_KINDS || !total_ms || !launches)
+    return fail(CX_EINVAL, "bad timing query");
   Timing& T = timing();
   std::vector<TimedLaunch> rec;
   {

@@ -68,8 +68,12 @@ struct SampleArgs {
   int32_t off_bitmap, off_hword, off_hval, off_hpen, off_wkey, off_widx, off_gather;
   int32_t lds_bytes;      // fused kernel dynamic LDS
   int32_t fin_lds_bytes;  // finish kernel dynamic LDS (several slices per row)
-  int32_t bf16;
+  int32_t bf16;           // logits are bf16 bit patterns
+  int32_t f64;            // logits are fp64 (exact multi-pass path only)
+  int32_t all_slow;       // every row takes the exact multi-pass path
   double logV;            // log(V)
+  double* out64;          // [B, ldo] fp64 output of the penalty and truncation kernels
+  int64_t ldo;
   int32_t slow_nbw;       // multi-pass kernel: full-row bitmap words (power of two)
   int32_t slow_off_hkey, slow_off_work, slow_off_tsum, slow_lds_bytes;
 };

@@ -35,6 +35,8 @@ struct SlowRow {
   const cx_row_params* P;
   const void* rowp;
   int bf16;
+  int f64;
+  bool direct;       // the row holds probabilities: value = mass, no penalties
   int V;
   bool pen;
   const uint32_t* bitmap;
@@ -45,15 +47,15 @@ struct SlowRow {
   double M, invT, S;
 };
 
-__device__ __forceinline__ float raw_at(const SlowRow& R, int i) {
-  return R.bf16 ? __uint_as_float((uint32_t)((const uint16_t*)R.rowp)[i] << 16)
-                : ((const float*)R.rowp)[i];
+__device__ __forceinline__ double raw_at(const SlowRow& R, int i) {
+  if (R.f64) return ((const double*)R.rowp)[i];
+  return R.bf16 ? (double)__uint_as_float((uint32_t)((const uint16_t*)R.rowp)[i] << 16)
+                : (double)((const float*)R.rowp)[i];
 }
 
 // Penalised fp64 value of element i (sampler.py:65-72 + presence/frequency).
 __device__ inline double value_at(const SlowRow& R, int i) {
-  float raw = raw_at(R, i);
-  double x = (double)raw;
+  double x = raw_at(R, i);
   if (R.pen && ((R.bitmap[(i >> 5) & (R.nbw - 1)] >> (i & 31)) & 1u)) {
     const uint32_t mask = (1u << R.ns_log2) - 1;
     uint32_t s = s_hash_slot(i, R.ns_log2);
@@ -75,7 +77,7 @@ __device__ inline double value_at(const SlowRow& R, int i) {
 }
 
 __device__ __forceinline__ double mass_of(const SlowRow& R, double v) {
-  return exp((v - R.M) * R.invT) / R.S;
+  return R.direct ? v : exp((v - R.M) * R.invT) / R.S;
 }
 
 // Boundary of a prefix in (key desc, idx asc) order: element e is inside iff
@@ -288,29 +290,32 @@ __device__ bool select_prefix(const SlowRow& R, const Filters& F, const Cut& eli
   return true;
 }
 
-// All WG threads of the workgroup; dyn holds the multi-pass layout (slow_*
-// offsets of SampleArgs).  Entered after a __syncthreads.
-__device__ inline void slow_row(const SampleArgs& A, int row, unsigned char* dyn,
-                                      double* red_d, int* red_i) {
-  double* tsum = (double*)(dyn + A.slow_off_tsum);
+// Row reader and penalty tables of one row (all WG threads; ends with a
+// __syncthreads when tables are built).  The window is the last
+// max(64, n_keep) history ids if n_keep > 0, else all of them
+// (sampler.py:67); ids outside [0, V) are ignored (:68).  Returns the
+// window length; a window longer than WIN_MAX builds no tables (the caller
+// reports the row as unsupported).
+__device__ inline int slow_setup(const SampleArgs& A, int row, const cx_row_params& P,
+                                 unsigned char* dyn, SlowRow& R) {
   const int t = threadIdx.x;
-  const cx_row_params P = A.prm[row];
   const int V = A.V;
-
-  SlowRow R;
   R.P = &P;
   R.bf16 = A.bf16;
+  R.f64 = A.f64;
+  R.direct = false;
   R.V = V;
-  R.rowp = (const char*)A.logits + (size_t)row * (size_t)A.ld * (A.bf16 ? 2 : 4);
-  // ---- penalty tables for the whole row
+  R.rowp = (const char*)A.logits +
+           (size_t)row * (size_t)A.ld * (A.f64 ? 8 : (A.bf16 ? 2 : 4));
   int wlen = 0, wstart = 0;
   if (A.ldh > 0) {
     int len = max(0, min(A.hist_len[row], (int)A.ldh));
     wstart = P.n_keep > 0 ? max(0, len - max(64, P.n_keep)) : 0;
     wlen = len - wstart;
   }
-  R.pen = wlen > 0 && (P.repetition_penalty != 1.0 || P.presence_penalty != 0.0 ||
-                       P.frequency_penalty != 0.0);
+  R.pen = wlen > 0 && wlen <= WIN_MAX &&
+          (P.repetition_penalty != 1.0 || P.presence_penalty != 0.0 ||
+           P.frequency_penalty != 0.0);
   uint32_t* bitmap = (uint32_t*)dyn;
   uint32_t* hkey = (uint32_t*)(dyn + A.slow_off_hkey);
   R.bitmap = bitmap;
@@ -318,6 +323,9 @@ __device__ inline void slow_row(const SampleArgs& A, int row, unsigned char* dyn
   R.hval = nullptr;
   R.nbw = A.slow_nbw;
   R.ns_log2 = A.ns_log2;
+  R.M = 0.0;
+  R.invT = 1.0;
+  R.S = 1.0;
   if (R.pen) {
     for (int i = t; i < R.nbw; i += WG) bitmap[i] = 0u;
     for (int i = t; i < A.ns; i += WG) hkey[i] = HEMPTY;
@@ -339,7 +347,10 @@ __device__ inline void slow_row(const SampleArgs& A, int row, unsigned char* dyn
     }
     __syncthreads();
   }
-  SlowLds L;
+  return wlen;
+}
+
+__device__ inline void slow_lds(const SampleArgs& A, unsigned char* dyn, SlowLds& L) {
   unsigned char* base = dyn + A.slow_off_work;
   L.cnt = (uint32_t*)base;
   L.mass = (double*)(base + NB * 4);
@@ -347,6 +358,28 @@ __device__ inline void slow_row(const SampleArgs& A, int row, unsigned char* dyn
   L.gi = (int32_t*)(base + NB * 12 + SCAP * 8);
   L.ga = (int32_t*)(base + NB * 12 + SCAP * 12);
   L.gm = (double*)(base + NB * 12 + SCAP * 16);
+}
+
+// All WG threads of the workgroup; dyn holds the multi-pass layout (slow_*
+// offsets of SampleArgs).  Entered after a __syncthreads.
+__device__ inline void slow_row(const SampleArgs& A, int row, unsigned char* dyn,
+                                      double* red_d, int* red_i) {
+  double* tsum = (double*)(dyn + A.slow_off_tsum);
+  const int t = threadIdx.x;
+  const cx_row_params P = A.prm[row];
+  const int V = A.V;
+
+  SlowRow R;
+  const int wlen = slow_setup(A, row, P, dyn, R);
+  if (wlen > WIN_MAX) {                     // window longer than the LDS index
+    if (t == 0) {
+      A.out_id[row] = -1;
+      A.row_status[row] = CX_ROW_UNSUPPORTED | CX_ROW_FLAG_SLOW;
+    }
+    return;
+  }
+  SlowLds L;
+  slow_lds(A, dyn, L);
 
   // ---- pass A: max, min, first argmax, first NaN
   double mx = -__builtin_inf(), mn = __builtin_inf();
@@ -364,6 +397,17 @@ __device__ inline void slow_row(const SampleArgs& A, int row, unsigned char* dyn
   mx = bv;
   mn = block_min(mn, red_d, __builtin_inf());
   const int amax = ni != INT_MAX ? ni : (bi == INT_MAX ? 0 : bi);
+  if (P.temperature == 0.0) {                                // sampler.py:114-115
+    if (A.out_probs) {
+      float* pr = A.out_probs + (size_t)row * V;
+      for (int i = t; i < V; i += WG) pr[i] = i == amax ? 1.0f : 0.0f;
+    }
+    if (t == 0) {
+      A.out_id[row] = amax;
+      A.row_status[row] = CX_ROW_GREEDY | CX_ROW_FLAG_SLOW;
+    }
+    return;
+  }
   const double invT = 1.0 / P.temperature;
   bool degenerate = ni != INT_MAX || mx == __builtin_inf() || mx == -__builtin_inf();
   R.M = mx;
@@ -507,6 +551,135 @@ __device__ inline void slow_row(const SampleArgs& A, int row, unsigned char* dyn
     A.out_id[row] = found;
     A.row_status[row] = CX_ROW_OK | CX_ROW_FLAG_SLOW;
   }
+}
+
+// Sampler.apply_penalties on elements [i0, i1) of a row (sampler.py:63-73,
+// plus presence/frequency): out64 = the fp64 penalised logits.  Every
+// workgroup of the row builds the row's tables; workgroup 0 writes the
+// row's status (CX_ROW_OK, or CX_ROW_UNSUPPORTED for a window longer than
+// WIN_MAX, with nothing written).
+__device__ inline void penalties_range(const SampleArgs& A, int row, int i0, int i1,
+                                       unsigned char* dyn, bool report) {
+  const cx_row_params P = A.prm[row];
+  SlowRow R;
+  const int wlen = slow_setup(A, row, P, dyn, R);
+  const bool ok = wlen <= WIN_MAX;
+  if (ok) {
+    double* out = A.out64 + (size_t)row * (size_t)A.ldo;
+    for (int i = i0 + (int)threadIdx.x; i < i1; i += WG) out[i] = value_at(R, i);
+  }
+  if (report && threadIdx.x == 0) A.row_status[row] = ok ? CX_ROW_OK : CX_ROW_UNSUPPORTED;
+}
+
+// Sampler._truncate on one row of fp64 probabilities (sampler.py:75-106).
+// The row's values are the masses themselves (no renormalisation, as in the
+// reference, whose top-p and typical cuts accumulate the unnormalised
+// input):
+//   top-k     keep P >= the k-th largest value (ties kept)         :76-79
+//   top-p     shortest prefix in (P desc, id asc) order whose
+//             running sum reaches top_p                           :81-89
+//   min-p     keep P >= min_p * max P                              :91-93
+//   typical   entropy H over the kept values, then the shortest
+//             prefix in (|log P + H| asc, id asc) order reaching
+//             typical_p                                            :95-105
+// out64[i] = P_i where kept, else 0.  Ties in the two orders go to the lower
+// id (numpy's argsort leaves their order unspecified).  A row holding NaN or
+// a negative value is reported as CX_ROW_ERROR and left unwritten.
+__device__ inline void truncate_row(const SampleArgs& A, int row, unsigned char* dyn,
+                                    double* red_d, int* red_i) {
+  const int t = threadIdx.x;
+  const cx_row_params P = A.prm[row];
+  const int V = A.V;
+  SlowRow R;
+  R.P = &P;
+  R.bf16 = 0;
+  R.f64 = 1;
+  R.direct = true;
+  R.V = V;
+  R.rowp = (const char*)A.logits + (size_t)row * (size_t)A.ld * 8;
+  R.pen = false;
+  R.bitmap = nullptr;
+  R.hkey = nullptr;
+  R.hval = nullptr;
+  R.nbw = 1;
+  R.ns_log2 = 0;
+  R.M = 0.0;
+  R.invT = 1.0;
+  R.S = 1.0;
+  SlowLds L;
+  slow_lds(A, dyn, L);
+
+  double mx = -__builtin_inf(), mn = __builtin_inf();
+  int bad = 0;
+  for (int i = t; i < V; i += WG) {
+    double v = value_at(R, i);
+    if (!(v >= 0.0)) { bad = 1; continue; }
+    mx = v > mx ? v : mx;
+    mn = v < mn ? v : mn;
+  }
+  bad = block_max(bad, red_i, 0);
+  mx = block_max(mx, red_d, -__builtin_inf());
+  mn = block_min(mn, red_d, __builtin_inf());
+  if (bad) {
+    if (t == 0) A.row_status[row] = CX_ROW_ERROR;
+    return;
+  }
+  Filters F;
+  F.rank.k = 0;
+  F.rank.i = INT_MAX;
+  F.floor_p = 0.0;
+  F.typ = false;
+  F.H = 0.0;
+  F.tcut.k = 0;
+  F.tcut.i = INT_MAX;
+  const uint64_t kmax = d2key(mx), kmin = d2key(mn);
+  Cut all;
+  all.k = 0;
+  all.i = INT_MAX;
+  if (P.top_k > 0 && P.top_k < V) {
+    Cut c;
+    select_prefix<false, false>(R, F, all, (double)P.top_k, kmin, kmax, L, c, red_d, red_i);
+    F.rank.k = c.k;
+    F.rank.i = INT_MAX;
+  }
+  if (P.top_p < 1.0) {
+    Cut c;
+    const uint64_t lo = F.rank.k > kmin ? F.rank.k : kmin;
+    if (select_prefix<false, true>(R, F, F.rank, P.top_p, lo, kmax, L, c, red_d, red_i))
+      F.rank = c;
+  }
+  if (P.min_p > 0.0) F.floor_p = P.min_p * mx;
+  if (P.typical_p < 1.0) {
+    double h = 0.0;
+    uint64_t tlo = ~0ull, thi = 0ull;
+    for (int i = t; i < V; i += WG) {
+      double p = value_at(R, i);
+      if (!kept_rank(F, d2key(p), i, p)) continue;
+      h -= p * log(p > 1e-38 ? p : 1e-38);
+    }
+    F.H = block_sum(h, red_d);
+    for (int i = t; i < V; i += WG) {
+      double p = value_at(R, i);
+      if (!kept_rank(F, d2key(p), i, p)) continue;
+      uint64_t k = typ_key(p, F.H);
+      tlo = k < tlo ? k : tlo;
+      thi = k > thi ? k : thi;
+    }
+    tlo = block_min<unsigned long long>(tlo, (unsigned long long*)red_d, ~0ull);
+    thi = block_max<unsigned long long>(thi, (unsigned long long*)red_d, 0ull);
+    Cut c = all;
+    if (tlo <= thi)
+      F.typ = select_prefix<true, true>(R, F, all, P.typical_p, tlo, thi, L, c, red_d, red_i);
+    F.tcut = c;
+  }
+  double* out = A.out64 + (size_t)row * (size_t)A.ldo;
+  for (int i = t; i < V; i += WG) {
+    double p = value_at(R, i);
+    bool keep = kept_rank(F, d2key(p), i, p);
+    if (keep && F.typ) keep = inside(F.tcut, typ_key(p, F.H), i);
+    out[i] = keep ? p : 0.0;
+  }
+  if (t == 0) A.row_status[row] = CX_ROW_OK;
 }
 
 }  // namespace cx

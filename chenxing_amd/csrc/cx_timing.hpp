@@ -9,6 +9,8 @@
 #include <mutex>
 #include <vector>
 
+#include "cx_sampler.h"
+
 namespace cx {
 
 struct TimedLaunch {
@@ -18,7 +20,7 @@ struct TimedLaunch {
 struct Timing {
   bool on = false;
   std::mutex mu;
-  std::vector<TimedLaunch> rec[5];
+  std::vector<TimedLaunch> rec[CX_KERNEL_KINDS];
   std::vector<hipEvent_t> pool;
 
   hipEvent_t take() {

@@ -1,0 +1,241 @@
+"""Drop-in ``Sampler`` with every computation on the device.
+
+Mirrors ``chenxing/core/sampler.py:46-127``: the same constructor, methods,
+return types and exceptions, so a caller of the reference (``engine.py:165``,
+``speculative.py:126,171``, ``scheduler.py:61``) can swap classes:
+
+  Sampler(vocab_size)
+  .sample(logits, params, generated_ids=None) -> int        sampler.py:108-127
+  .apply_penalties(logits, params, generated_ids) -> fp64   sampler.py:63-73
+  ._truncate(probs, params) -> fp64                         sampler.py:75-106
+  ._rng, ._rng_for(seed)                                    sampler.py:54-61
+
+plus ``sample_batch`` for a decode batch in one launch.  The arithmetic runs
+in the HIP library (``include/cx_sampler.h``); this module only marshals
+arguments, supplies the uniforms and maps row outcomes to the reference's
+exceptions.  Without the built library every method raises.
+
+Uniforms.  The reference draws exactly one variate, inside
+``Generator.choice``, and only on rows that reach it: greedy rows, rows whose
+filtered mass is zero (argmax fallback) and rows numpy rejects draw nothing.
+A seeded call uses a fresh ``default_rng(seed)``; an unseeded one the
+sampler's own generator.  Here the next variate is read before the launch
+and the generator is rewound when the device reports that the row did not
+draw, so the generator advances exactly as the reference's does.
+"""
+from __future__ import annotations
+
+import threading
+from typing import Sequence
+
+import numpy as np
+
+from . import _lib
+from .params import RowParams, SamplingParams, pack_rows
+
+__all__ = ["Sampler", "SamplingParams"]
+
+# Longest penalty window the device holds (distinct ids when only the
+# repetition and presence penalties are on).
+WINDOW_MAX = 4095
+
+_NUMPY_NAN = "probabilities contain NaN"          # numpy Generator.choice's message
+_NUMPY_SIZE = "'a' and 'p' must have same size"
+
+
+def _is_torch_cuda(x) -> bool:
+    try:
+        import torch
+    except ImportError:
+        return False
+    return isinstance(x, torch.Tensor) and x.is_cuda
+
+
+class Sampler:
+    """Logits processor + sampler (sampler.py:46-127) on the GPU."""
+
+    def __init__(self, vocab_size: int) -> None:
+        self.vocab_size = vocab_size
+        self._rng = np.random.default_rng()
+        self._lock = threading.Lock()
+        _lib.load()
+
+    def _rng_for(self, seed: int | None) -> np.random.Generator:
+        if seed is None:
+            return self._rng
+        return np.random.default_rng(seed)
+
+    # ------------------------------------------------------------ arguments
+    def _window(self, params, generated_ids, V: int):
+        """The history handed to the device for one row: the reference's
+        penalty window (sampler.py:67) with ids outside [0, vocab_size)
+        replaced by -1 (:68).  None when no penalty is on."""
+        rp = float(params.repetition_penalty)
+        pres = float(getattr(params, "presence_penalty", 0.0))
+        freq = float(getattr(params, "frequency_penalty", 0.0))
+        if not generated_ids or (rp == 1.0 and pres == 0.0 and freq == 0.0):
+            return None
+        n_keep = int(getattr(params, "n_keep", 0))
+        win = list(generated_ids[-max(64, n_keep):]) if n_keep else list(generated_ids)
+        try:
+            h = np.asarray(win, dtype=np.int64)
+        except OverflowError:
+            h = np.asarray([t if -1 <= t < 2**62 else -1 for t in win], dtype=np.int64)
+        inr = (h >= 0) & (h < self.vocab_size)
+        if rp != 1.0 and np.any(inr & (h >= V)):
+            # the reference indexes the row with every in-range id
+            bad = int(h[inr & (h >= V)][0])
+            raise IndexError(f"index {bad} is out of bounds for axis 0 with size {V}")
+        h = np.where(inr & (h < V), h, -1)
+        if h.size > WINDOW_MAX:
+            if freq != 0.0:
+                raise ValueError(f"frequency penalty over a window of {h.size} ids: the "
+                                 f"device holds at most {WINDOW_MAX}")
+            # repetition and presence penalties depend on the set of ids only
+            h = np.unique(h[h >= 0])
+            if h.size > WINDOW_MAX:
+                raise ValueError(f"penalty window holds {h.size} distinct ids: the device "
+                                 f"holds at most {WINDOW_MAX}")
+        return h.astype(np.int32)
+
+    @staticmethod
+    def _as_row(logits) -> tuple[np.ndarray, bool]:
+        x = np.asarray(logits)
+        if x.ndim != 1:
+            raise ValueError("logits must be a 1-D row")
+        if x.dtype not in (np.float32, np.float64):
+            x = x.astype(np.float64)            # the reference's first step (sampler.py:65)
+        return np.ascontiguousarray(x), False
+
+    # ------------------------------------------------------------ reference API
+    def apply_penalties(self, logits: np.ndarray, params,
+                        generated_ids: list[int]) -> np.ndarray:
+        """fp64 copy of the row with the penalties applied (sampler.py:63-73)."""
+        x, _ = self._as_row(logits)
+        win = self._window(params, generated_ids, x.size)
+        hist = None if win is None else win[None]
+        out, st = _lib.apply_penalties_host(x[None], [RowParams.of(params)], hist)
+        if st[0] != _lib.ROW_OK:
+            raise ValueError(f"apply_penalties: device status {int(st[0])}")
+        return out[0]
+
+    def _truncate(self, probs: np.ndarray, params) -> np.ndarray:
+        """top-k / top-p / min-p / typical-p filter (sampler.py:75-106): the
+        input values where kept, zero elsewhere; not renormalised."""
+        p = np.asarray(probs, dtype=np.float64)
+        if p.ndim != 1:
+            raise ValueError("probs must be a 1-D row")
+        out, st = _lib.truncate_host(p[None], [RowParams.of(params)])
+        if st[0] != _lib.ROW_OK:
+            raise ValueError("_truncate expects finite, non-negative probabilities")
+        return out[0]
+
+    def sample(self, logits: np.ndarray, params,
+               generated_ids: list[int] | None = None) -> int:
+        """Draw one token id from ``logits`` (1-D, vocab size) (sampler.py:108-127)."""
+        if _is_torch_cuda(logits):
+            return self.sample_batch(logits.reshape(1, -1), [params],
+                                     [generated_ids or []])[0]
+        x, _ = self._as_row(logits)
+        return self.sample_batch(x[None], [params], [generated_ids or []])[0]
+
+    # ------------------------------------------------------------ batched
+    def sample_batch(self, logits, params: Sequence | object,
+                     generated_ids: Sequence[Sequence[int]] | None = None) -> list[int]:
+        """``sample`` for every row of ``logits`` [B, V] in one launch.
+
+        Equivalent to ``[self.sample(logits[b], params[b], generated_ids[b])
+        for b in range(B)]``, including the order in which rows draw from
+        the sampler's generator and the exception the first failing row
+        raises.  ``logits`` is a numpy array (float32 or float64) or a CUDA
+        tensor (float32, bfloat16 or float64) that stays on the device.
+        """
+        on_dev = _is_torch_cuda(logits)
+        if on_dev:
+            B, V = int(logits.shape[0]), int(logits.shape[1])
+        else:
+            x = np.asarray(logits)
+            if x.ndim != 2:
+                raise ValueError("logits must be [B, V]")
+            if x.dtype not in (np.float32, np.float64):
+                x = x.astype(np.float64)
+            x = np.ascontiguousarray(x)
+            B, V = x.shape
+        plist = list(params) if isinstance(params, (list, tuple)) else [params] * B
+        if len(plist) != B:
+            raise ValueError("need one SamplingParams per row")
+        hists = list(generated_ids) if generated_ids is not None else [[]] * B
+        if len(hists) != B:
+            raise ValueError("need one history per row")
+        if B == 0:
+            return []
+        wins = [self._window(p, h or [], V) for p, h in zip(plist, hists)]
+        H = max((w.size for w in wins if w is not None), default=0)
+        hist = hist_len = None
+        if H > 0:
+            hist = np.full((B, H), -1, np.int32)
+            hist_len = np.zeros(B, np.int32)
+            for b, w in enumerate(wins):
+                if w is not None:
+                    hist[b, :w.size] = w
+                    hist_len[b] = w.size
+        prm = pack_rows(plist)
+        stoch = [float(p.temperature) != 0.0 for p in plist]
+        seeds = [getattr(p, "seed", None) for p in plist]
+
+        def run(u):
+            if on_dev:
+                return self._run_device(logits, prm, u, hist, hist_len)
+            ids, st, _ = _lib.sample_host(x, prm, hist, hist_len, u)
+            return ids, st
+
+        with self._lock:
+            state = self._rng.bit_generator.state
+            u = self._uniforms(stoch, seeds, None)
+            ids, st = run(u)
+            draws = [(int(s) & 0xFF) == _lib.ROW_OK for s in st]
+            if any(stoch[b] and seeds[b] is None and not draws[b] for b in range(B)):
+                # a row that draws nothing must not take a variate from the
+                # shared generator: hand the variates to the drawing rows only
+                self._rng.bit_generator.state = state
+                u = self._uniforms(stoch, seeds, draws)
+                ids, st = run(u)
+            out = []
+            self._rng.bit_generator.state = state
+            for b in range(B):
+                code = int(st[b]) & 0xFF
+                if code == _lib.ROW_OK and V != self.vocab_size:
+                    raise ValueError(_NUMPY_SIZE)      # choice(vocab_size, p) (:127)
+                if code == _lib.ROW_ERROR:
+                    raise ValueError(_NUMPY_NAN)
+                if code == _lib.ROW_UNSUPPORTED:
+                    raise ValueError("row outside the sampler library's limits")
+                if code == _lib.ROW_OK and seeds[b] is None:
+                    self._rng.random()                 # the variate this row drew
+                out.append(int(ids[b]))
+            return out
+
+    def _uniforms(self, stoch, seeds, draws) -> np.ndarray:
+        """One variate per row: fresh default_rng(seed) for seeded rows, the
+        shared generator's next variate (in row order) for unseeded rows that
+        draw (all stochastic rows when ``draws`` is None)."""
+        u = np.zeros(len(stoch))
+        for b, s in enumerate(stoch):
+            if not s or (draws is not None and not draws[b]):
+                continue
+            u[b] = np.random.default_rng(seeds[b]).random() if seeds[b] is not None \
+                else self._rng.random()
+        return u
+
+    @staticmethod
+    def _run_device(logits, prm: np.ndarray, u: np.ndarray, hist, hist_len):
+        import torch
+        dev = logits.device
+        prm_d = torch.from_numpy(prm.view(np.uint8).copy()).to(dev)
+        u_d = torch.from_numpy(u).to(dev)
+        h_d = hl_d = None
+        if hist is not None:
+            h_d = torch.from_numpy(hist).to(dev)
+            hl_d = torch.from_numpy(hist_len).to(dev)
+        ids, st = _lib.sample_device(logits, prm_d, u_d, h_d, hl_d)
+        return ids.cpu().numpy(), st.cpu().numpy()

@@ -50,6 +50,11 @@ class SpeculativeStats:
         }
 
 
+# Greedy draft proposals are ``int(np.argmax(q_row))`` (speculative.py:125):
+# the draft engine's sampler at T = 0 with no history computes exactly that.
+_GREEDY = SamplingParams(temperature=0.0)
+
+
 class DeviceVerifier:
     """One verify round through ``cx_spec_verify_f32_host``."""
 
@@ -95,7 +100,7 @@ class SpeculativeDecoder:
         q_rows.append(self.draft.forward_ids(dseq, [confirmed[n_start]],
                                              allow_unconfirmed=True)[-1])
         for i in range(self.k_draft):
-            tok = int(np.argmax(q_rows[-1])) if greedy else \
+            tok = self.draft.sampler.sample(q_rows[-1], _GREEDY) if greedy else \
                 self.draft.sampler.sample(q_rows[-1], params, confirmed)
             proposed.append(tok)
             self.stats.drafted += 1

@@ -91,14 +91,64 @@ int cx_sample_bf16(const uint16_t* logits, int64_t ld, int32_t B, int32_t V,
                    int32_t* out_id, int32_t* row_status, float* out_probs,
                    void* workspace, size_t ws_bytes, void* stream);
 
+/* fp64 logits (the reference's Sampler.sample takes any float row; its model
+ * produces fp32).  Same contract as cx_sample_f32; every row runs the exact
+ * multi-pass fp64 path (slower than the fused fp32 / bf16 kernel). */
+int cx_sample_f64(const double* logits, int64_t ld, int32_t B, int32_t V,
+                  const int32_t* hist, const int32_t* hist_len, int64_t ldh,
+                  const cx_row_params* prm, const double* u,
+                  int32_t* out_id, int32_t* row_status, float* out_probs,
+                  void* workspace, size_t ws_bytes, void* stream);
+
 size_t cx_sample_workspace_bytes(int32_t B, int32_t V, int64_t ldh);
 
 /* Host-memory variants: same arguments on host memory; allocate, copy,
- * launch, copy back and synchronise.  dtype: 0 = fp32, 1 = bf16. */
+ * launch, copy back and synchronise.  dtype: 0 = fp32, 1 = bf16, 2 = fp64. */
 int cx_sample_host(const void* logits, int32_t dtype, int64_t ld, int32_t B, int32_t V,
                    const int32_t* hist, const int32_t* hist_len, int64_t ldh,
                    const cx_row_params* prm, const double* u,
                    int32_t* out_id, int32_t* row_status, float* out_probs);
+
+/*
+ * Sampler.apply_penalties (sampler.py:63-73) for a batch of rows: out[b] is
+ * float64(logits[b]) with the repetition penalty (x / rp if x > 0 else
+ * x * rp, once per distinct in-range id of the window) and then the
+ * presence / frequency penalties applied.  The window and id filtering are
+ * those of cx_sample_f32.  Never writes the logits.
+ *
+ *  logits     [B, ld] of dtype 0 = fp32, 1 = bf16 bit patterns, 2 = fp64
+ *  out        [B, ldo] fp64
+ *  row_status [B] CX_ROW_OK, or CX_ROW_UNSUPPORTED when the row's window is
+ *             longer than 4095 ids (out[b] is then not written)
+ * No workspace; stream-ordered, never synchronises.
+ */
+int cx_apply_penalties(const void* logits, int32_t dtype, int64_t ld, int32_t B, int32_t V,
+                       const int32_t* hist, const int32_t* hist_len, int64_t ldh,
+                       const cx_row_params* prm, double* out, int64_t ldo,
+                       int32_t* row_status, void* stream);
+
+int cx_apply_penalties_host(const void* logits, int32_t dtype, int64_t ld, int32_t B, int32_t V,
+                            const int32_t* hist, const int32_t* hist_len, int64_t ldh,
+                            const cx_row_params* prm, double* out, int32_t* row_status);
+
+/*
+ * Sampler._truncate (sampler.py:75-106) for a batch of rows of fp64
+ * probabilities: top-k (ties kept), top-p, min-p and typical-p on the
+ * values as given (not renormalised, as the reference does), in that order.
+ * out[b, i] = probs[b, i] where kept, else 0.  Equal values are ordered by
+ * ascending id in the top-p and typical orders (numpy's argsort leaves that
+ * order unspecified).  Uses temperature-independent fields of prm only.
+ *
+ *  row_status [B] CX_ROW_OK, or CX_ROW_ERROR for a row holding NaN or a
+ *             negative value (out[b] is then not written)
+ * No workspace; stream-ordered, never synchronises.
+ */
+int cx_truncate_f64(const double* probs, int64_t ld, int32_t B, int32_t V,
+                    const cx_row_params* prm, double* out, int64_t ldo,
+                    int32_t* row_status, void* stream);
+
+int cx_truncate_host(const double* probs, int64_t ld, int32_t B, int32_t V,
+                     const cx_row_params* prm, double* out, int32_t* row_status);
 
 /*
  * Speculative-decoding verify step (speculative.py:145-171, with _softmax
@@ -146,6 +196,9 @@ int cx_spec_verify_host(const float* target, const float* draft, const int32_t* 
 #define CX_KERNEL_VERIFY_STATS  2  /* verify: stats over all rows     */
 #define CX_KERNEL_VERIFY_REST   3  /* verify: decide + residual draw  */
 #define CX_KERNEL_SAMPLE_FINISH 4  /* sampler finisher (rows in several slices) */
+#define CX_KERNEL_PENALTIES     5  /* apply_penalties                 */
+#define CX_KERNEL_TRUNCATE      6  /* _truncate                       */
+#define CX_KERNEL_KINDS         7
 int cx_timing_enable(int on);
 int cx_timing_read(int32_t kernel, double* total_ms, int64_t* launches);
 

@@ -1,0 +1,65 @@
+"""Host logic of the drop-in Sampler (no device calls): argument checks,
+the penalty window handed to the device, parameter validation."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from chenxing_amd import Sampler, SamplingParams
+
+
+def test_invalid_params_raise():                       # chenxing tests/test_sampler.py:64-69
+    with pytest.raises(ValueError):
+        SamplingParams(top_p=1.5)
+    with pytest.raises(ValueError):
+        SamplingParams(temperature=-1)
+    with pytest.raises(ValueError):
+        SamplingParams(min_p=-0.1)
+
+
+def test_window_is_none_without_penalties():
+    s = Sampler(10)
+    assert s._window(SamplingParams(), [1, 2, 3], 10) is None
+    assert s._window(SamplingParams(repetition_penalty=1.2), [], 10) is None
+
+
+def test_window_follows_n_keep_and_drops_out_of_range_ids():
+    s = Sampler(10)
+    h = list(range(-3, 200))                            # 203 ids, most out of range
+    w = s._window(SamplingParams(repetition_penalty=1.2, n_keep=70), h, 10)
+    assert w.size == 70                                 # last max(64, n_keep) ids (sampler.py:67)
+    assert np.all(w == -1)                              # 130..199 are >= vocab_size (:68)
+    w = s._window(SamplingParams(repetition_penalty=1.2), [-1, 0, 9, 10, 3], 10)
+    assert w.tolist() == [-1, 0, 9, -1, 3]
+    w = s._window(SamplingParams(repetition_penalty=1.2, n_keep=3), list(range(100)), 10)
+    assert w.size == 64                                 # max(64, 3)
+
+
+def test_window_index_error_like_the_reference():
+    # vocab_size larger than the row: the reference indexes the row with the id
+    s = Sampler(20)
+    with pytest.raises(IndexError):
+        s._window(SamplingParams(repetition_penalty=1.2), [15], 10)
+    # without the repetition penalty nothing is indexed
+    assert s._window(SamplingParams(presence_penalty=0.5), [15], 10).tolist() == [-1]
+
+
+def test_long_window_deduplicated_when_counts_do_not_matter():
+    s = Sampler(100)
+    h = [i % 50 for i in range(10_000)]
+    w = s._window(SamplingParams(repetition_penalty=1.1, presence_penalty=0.2), h, 100)
+    assert sorted(w.tolist()) == list(range(50))
+    with pytest.raises(ValueError):
+        s._window(SamplingParams(frequency_penalty=0.1), h, 100)
+    with pytest.raises(ValueError):
+        Sampler(10_000)._window(SamplingParams(repetition_penalty=1.1), list(range(5000)),
+                                10_000)
+
+
+def test_batch_argument_checks():
+    s = Sampler(8)
+    with pytest.raises(ValueError):
+        s.sample(np.zeros((2, 8), np.float32), SamplingParams())
+    with pytest.raises(ValueError):
+        s.sample_batch(np.zeros((2, 8), np.float32), [SamplingParams()] * 3)
+    assert s.sample_batch(np.zeros((0, 8), np.float32), []) == []
