@@ -114,7 +114,7 @@ def time_steps(fn, steps: int, warmup: int, kernel: int):
     torch.cuda.synchronize()
     _lib.timing_enable(False)
     kms, n = _lib.timing_read(kernel)
-    for k in range(5):
+    for k in range(7):
         _lib.timing_read(k)
     return step_ms, kms / max(n, 1)
 
@@ -174,6 +174,39 @@ def cpu_baseline_pool(w, rows_per_worker: int, workers: int) -> dict:
                       f"({dt:.1f} s, numpy {np.__version__}, {_cpu_model()})"}
 
 
+OTHER = {  # name: (workload factory, kernel whose launches are timed)
+    "nucleus": ("nucleus", {}, 0),
+    "nucleus_greedy": ("nucleus", {"greedy": True}, 0),
+    "hetero_bf16": ("hetero_bf16", {}, 0),
+    "spec_verify": ("spec_verify", {}, 2),
+    "spec_verify_greedy": ("spec_verify", {"greedy": True}, 2),
+}
+
+
+def time_other(name: str, dev, steps: int, warmup: int) -> dict:
+    import torch
+    from chenxing_amd import _lib, workloads as W
+    fac, kw, kernel = OTHER[name]
+    wk = getattr(W, fac)(**kw)
+    if name.startswith("spec"):
+        fn = DeviceVerify(wk, dev)
+        nb = W.verify_algorithmic_bytes(wk)
+        rows = wk.target.shape[0]
+    else:
+        fn = DeviceSample(wk, dev)
+        nb = W.algorithmic_bytes(wk)
+        rows = wk.B
+    sm, km = time_steps(fn, steps, warmup, kernel)
+    entry = {"rows_per_s": round(rows / (sm / 1e3), 1), "ms_per_step": round(sm, 5),
+             "algorithmic_bytes": nb, "step_GBps": round(nb / (sm / 1e3) / 1e9, 1),
+             "main_kernel_ms": round(km, 5)}
+    if not name.startswith("spec"):
+        entry["slow_path_rows"] = int(np.sum((fn.st.cpu().numpy() & 0x100) != 0))
+    del fn
+    torch.cuda.empty_cache()
+    return entry
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -181,6 +214,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--quick", action="store_true", help="headline workload only")
+    ap.add_argument("--only", choices=list(OTHER),
+                    help="time one of the other workloads alone and print its entry "
+                         "(for profiling that workload)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a plain 512 MiB device copy (torch copy_) 5 times: the "
                          "reference kernel for scaling FETCH_SIZE / WRITE_SIZE counters")
@@ -193,6 +229,14 @@ def main() -> int:
         return 2
 
     from chenxing_amd import workloads as W
+    if args.only:
+        import torch
+        from chenxing_amd import _lib
+        _lib.load()
+        _say(f"[bench] {args.only}")
+        entry = time_other(args.only, torch.device("cuda:0"), args.steps, args.warmup)
+        print(json.dumps({"workload": args.only, "steps": args.steps, **entry}), flush=True)
+        return 0
     _say("[bench] generating full_penalty workload")
     w = W.full_penalty()
 
@@ -229,33 +273,10 @@ def main() -> int:
 
     other = {}
     if not args.quick:
-        specs = [("nucleus", lambda: W.nucleus(), _lib.KERNEL_SAMPLE),
-                 ("nucleus_greedy", lambda: W.nucleus(greedy=True), _lib.KERNEL_SAMPLE),
-                 ("hetero_bf16", lambda: W.hetero_bf16(), _lib.KERNEL_SAMPLE),
-                 ("spec_verify", lambda: W.spec_verify(), _lib.KERNEL_VERIFY_STATS),
-                 ("spec_verify_greedy", lambda: W.spec_verify(greedy=True),
-                  _lib.KERNEL_VERIFY_STATS)]
-        for name, make, kernel in specs:
+        for name in OTHER:
             _say(f"[bench] {name}")
-            wk = make()
-            if name.startswith("spec"):
-                fn = DeviceVerify(wk, dev)
-                nb = W.verify_algorithmic_bytes(wk)
-                rows = wk.target.shape[0]
-            else:
-                fn = DeviceSample(wk, dev)
-                nb = W.algorithmic_bytes(wk)
-                rows = wk.B
-            steps = max(20, args.steps // 5)
-            sm, km = time_steps(fn, steps, max(5, args.warmup // 5), kernel)
-            entry = {"rows_per_s": round(rows / (sm / 1e3), 1), "ms_per_step": round(sm, 5),
-                     "algorithmic_bytes": nb, "step_GBps": round(nb / (sm / 1e3) / 1e9, 1),
-                     "main_kernel_ms": round(km, 5)}
-            if not name.startswith("spec"):
-                entry["slow_path_rows"] = int(np.sum((fn.st.cpu().numpy() & 0x100) != 0))
-            other[name] = entry
-            del fn
-            torch.cuda.empty_cache()
+            other[name] = time_other(name, dev, max(20, args.steps // 5),
+                                     max(5, args.warmup // 5))
 
     if args.copy_probe:
         _say("[bench] copy probe: 5 x 512 MiB device copy")

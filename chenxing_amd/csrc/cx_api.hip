@@ -199,6 +199,8 @@ static int verify_impl(const float* target, const float* draft, const int32_t* i
                        void* ws, size_t ws_bytes, void* stream, bool any_stoch) {
   g_err.clear();
   if (B < 0 || gamma < 1 || V < 1) return fail(CX_EINVAL, "bad shape B=%d gamma=%d V=%d", B, gamma, V);
+  if (gamma > GAMMA_MAX) return fail(CX_EINVAL, "gamma=%d exceeds %d", gamma, GAMMA_MAX);
+  if (V > 2 * WG * SUB) return fail(CX_EINVAL, "V=%d exceeds %d", V, 2 * WG * SUB);
   if (B == 0) return CX_OK;
   if (!target || !ids || !u || !temp || !accepted || !next_tok || !used || !status || !ws)
     return fail(CX_EINVAL, "null pointer argument");
@@ -217,6 +219,8 @@ static int verify_impl(const float* target, const float* draft, const int32_t* i
   A.gamma = gamma;
   A.V = V;
   A.nchunk = (V + VCHUNK - 1) / VCHUNK;
+  A.nsub = (V + SUB - 1) / SUB;
+  A.draft_rows = any_stoch ? 1 : 0;
   A.accepted = accepted;
   A.next_tok = next_tok;
   A.used = used;
@@ -224,7 +228,8 @@ static int verify_impl(const float* target, const float* draft, const int32_t* i
   char* w = (char*)ws;
   A.cstats = (ChunkStats*)(w + L.off_cstats);
   A.seq = (SeqState*)(w + L.off_seq);
-  A.rmass = (double*)(w + L.off_rmass);
+  A.npart = (NormPart*)(w + L.off_npart);
+  A.amb = (AmbEntry*)(w + L.off_amb);
   int e = launch_verify(A, any_stoch, (hipStream_t)stream);
   if (e != 0) return hip_fail((hipError_t)e, "verify launch");
   return CX_OK;

@@ -389,4 +389,61 @@ __device__ inline void block_scan(double* v, int n, double* scratch) {
   __syncthreads();
 }
 
+
+// ------------------------------------------------------------ fp64 exp
+// 2^(j/64), j = 0..63, each correctly rounded to fp64.
+static __device__ const double EXP64_TAB[64] = {
+    1.0, 1.0108892860517005, 1.0218971486541166, 1.0330248790212284,
+    1.0442737824274138, 1.0556451783605572, 1.0671404006768237, 1.0787607977571199,
+    1.0905077326652577, 1.102382583307841, 1.1143867425958924, 1.1265216186082418,
+    1.1387886347566916, 1.1511892299529827, 1.1637248587775775, 1.1763969916502812,
+    1.189207115002721, 1.202156731452703, 1.215247359980469, 1.22848053610687,
+    1.241857812073484, 1.255380757024691, 1.2690509571917332, 1.2828700160787783,
+    1.2968395546510096, 1.3109612115247644, 1.3252366431597413, 1.339667524053303,
+    1.3542555469368927, 1.3690024229745905, 1.383909881963832, 1.3989796725383112,
+    1.4142135623730951, 1.42961333839197, 1.4451808069770467, 1.460917794180647,
+    1.4768261459394993, 1.4929077282912648, 1.5091644275934228, 1.5255981507445384,
+    1.5422108254079407, 1.559004400237837, 1.5759808451078865, 1.593142151342267,
+    1.6104903319492543, 1.6280274218573478, 1.645755478153965, 1.6636765803267364,
+    1.681792830507429, 1.7001063537185235, 1.718619298122478, 1.7373338352737062,
+    1.7562521603732995, 1.7753764925265212, 1.7947090750031072, 1.8142521755003989,
+    1.8340080864093424, 1.8539791250833855, 1.8741676341103, 1.8945759815869656,
+    1.9152065613971474, 1.9360617934922943, 1.9571441241754002, 1.978456026387951,
+};
+
+// Copy EXP64_TAB into an LDS array of 64 doubles (all threads; ends with a
+// barrier).
+__device__ __forceinline__ void load_exp64_tab(double* lds_tab) {
+  if (threadIdx.x < 64) lds_tab[threadIdx.x] = EXP64_TAB[threadIdx.x];
+  __syncthreads();
+}
+
+// exp(x) in fp64 within 1 ulp, by Tang's table-driven method (P. T. P. Tang,
+// ACM TOMS 15(2), 1989): x = (64 m + j) ln2/64 + r with |r| <= ln2/128, so
+// exp(x) = 2^m 2^(j/64) exp(r), and exp(r) - 1 is its degree-5 Taylor
+// polynomial (truncation below 4e-17).  ln2/64 is split into a 36-bit head,
+// so k * head is exact for |k| < 2^17, and a tail.  `tab` is EXP64_TAB in
+// LDS.  Branch-free, so several calls interleave: x < -745.2 (and -inf)
+// gives 0, NaN gives NaN; meant for x <= 709.
+__device__ __forceinline__ double exp64(double x, const double* tab) {
+  const double xc = __builtin_fmin(__builtin_fmax(x, -745.2), 709.0);   // NaN -> -745.2
+  const double kd = __builtin_rint(xc * 92.33248261689366);     // xc * 64 / ln2
+  double r = __builtin_fma(-kd, 0.010830424696223417, xc);      // head of ln2/64
+  r = __builtin_fma(-kd, 2.572804622327669e-14, r);             // tail of ln2/64
+  const int k = (int)kd;
+  const double p = r * __builtin_fma(r, __builtin_fma(r, __builtin_fma(r, __builtin_fma(
+                           r, 1.0 / 120.0, 1.0 / 24.0), 1.0 / 6.0), 0.5), 1.0);
+  const double t = tab[k & 63];
+  const double v = __builtin_ldexp(__builtin_fma(t, p, t), k >> 6);
+  return x > -745.2 ? v : (x != x ? x : 0.0);
+}
+
+// fl32(x / T) for fp32 x and T, given invT = 1 / (double)T: the fp64 product
+// is within 2^-52 of x / T, and a quotient of two fp32 values that is not a
+// midpoint of fp32 lies at least 2^-48 (relative) from one, so rounding the
+// product to fp32 gives the correctly rounded fp32 quotient.
+__device__ __forceinline__ double div32(float x, double invT) {
+  return (double)(float)((double)x * invT);
+}
+
 }  // namespace cx

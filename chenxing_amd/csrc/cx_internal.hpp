@@ -79,7 +79,8 @@ struct SampleArgs {
 };
 
 // ---------------------------------------------------------------- verify
-constexpr int VCHUNK = 32768;          // elements per verify stats / residual chunk
+constexpr int VCHUNK = 32768;          // elements per verify stats chunk
+constexpr int GAMMA_MAX = 256;         // longest draft the verify kernels accept
 
 struct ChunkStats {                    // 32 bytes per (row, chunk)
   float m;                             // chunk max of x (stochastic rows)
@@ -87,17 +88,42 @@ struct ChunkStats {                    // 32 bytes per (row, chunk)
   int32_t bi;
   int32_t nan_i;
   double s;                            // sum exp2((x - m) * c)
-  double pad;
+  float xt;                            // the row's logit at the drafted token, if in this chunk
+  int32_t has_xt;
 };
 
 struct SeqState {                      // 64 bytes per sequence
   int32_t accepted, next_tok, used, status;
-  int32_t rej;                         // rejected position, -1 if none
+  int32_t rej1;                        // rejected position + 1; 0 if none
   int32_t exact;                       // normalisers below are exact fp64
   float Mt, Mq;                        // row maxima of x at position rej
   double St, Sq;                       // normalisers at position rej
   double R, pad;
 };
+
+static_assert(sizeof(ChunkStats) == 32, "ChunkStats layout");
+static_assert(sizeof(SeqState) == 64, "SeqState layout");
+
+constexpr int SUB = 512;               // elements per normaliser partial: one wave, 8 per lane
+constexpr int AMB_CAP = 8;             // undecided residual signs kept per partial
+
+// Exact normaliser partials of the rejected position's row pair over one
+// 512-element sub-chunk, with e = exp(z_t - max z_t), f = exp(z_q - max z_q)
+// and lam0 the normalisers' ratio known before the pass: the residual
+// max(e / St - f / Sq, 0) is St^-1 max(e - lam f, 0) with lam = St / Sq,
+// positive for sure where e > lam0 (1 + eps) f, zero where
+// e < lam0 (1 - eps) f, and undecided (listed) in between.
+struct NormPart {                      // 64 bytes per (sequence, sub-chunk)
+  double se, sf;                       // sum e, sum f
+  double dp;                           // sum over sure-positive elements of e - lam0 f
+  double fp;                           // sum over sure-positive elements of f
+  int32_t namb;                        // undecided elements (> AMB_CAP: list overflowed)
+  int32_t pad[7];
+};
+struct AmbEntry {                      // 16 bytes
+  double e, f;
+};
+static_assert(sizeof(NormPart) == 64, "NormPart layout");
 
 struct VerifyArgs {
   const float* target;
@@ -105,14 +131,16 @@ struct VerifyArgs {
   const int32_t* draft_ids;
   const double* u;
   const float* temperature;
-  int32_t B, gamma, V, nchunk;
+  int32_t B, gamma, V, nchunk, nsub;
+  int32_t draft_rows;                  // the stats grid includes the draft rows
   int32_t* accepted;
   int32_t* next_tok;
   int32_t* used;
   int32_t* row_status;
   ChunkStats* cstats;                  // [(B*(gamma+1) + B*gamma) * nchunk]
   SeqState* seq;                       // [B]
-  double* rmass;                       // [B * nchunk]
+  NormPart* npart;                     // [B * nsub]
+  AmbEntry* amb;                       // [B * nsub * AMB_CAP]
 };
 
 // Workspace layout (bytes), identical on host and device.
@@ -138,17 +166,19 @@ inline int choose_nsplit(int B, int V) {
 }
 
 struct VerifyWorkspace {
-  size_t off_cstats, off_seq, off_rmass, total;
+  size_t off_cstats, off_seq, off_npart, off_amb, total;
 };
 
 inline VerifyWorkspace verify_workspace_layout(int B, int gamma, int V) {
   VerifyWorkspace w;
   int nchunk = (V + VCHUNK - 1) / VCHUNK;
+  int nsub = (V + SUB - 1) / SUB;
   size_t rows = (size_t)B * (gamma + 1) + (size_t)B * gamma;
   w.off_cstats = 0;
   w.off_seq = align_up(rows * nchunk * sizeof(ChunkStats), 256);
-  w.off_rmass = align_up(w.off_seq + (size_t)B * sizeof(SeqState), 256);
-  w.total = align_up(w.off_rmass + (size_t)B * nchunk * sizeof(double), 256);
+  w.off_npart = align_up(w.off_seq + (size_t)B * sizeof(SeqState), 256);
+  w.off_amb = align_up(w.off_npart + (size_t)B * nsub * sizeof(NormPart), 256);
+  w.total = align_up(w.off_amb + (size_t)B * nsub * AMB_CAP * sizeof(AmbEntry), 256);
   return w;
 }
 

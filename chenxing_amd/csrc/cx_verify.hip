@@ -4,21 +4,31 @@
 // The reference walks the gamma draft positions serially and stops at the
 // first rejection.  Every position's accept test depends only on its own
 // target/draft row pair and its own uniform, so the device evaluates all
-// positions in parallel and then takes the first rejection:
+// positions in parallel and then takes the first rejection.  Four launches,
+// each reading what the previous one wrote:
 //
-//   1. verify_stats    grid (rows x chunks): one HBM read of every target
-//                      and draft row; per chunk the row max and
-//                      sum exp((x - m) / T) (fp32 exp2 terms, fp64 sums), or
-//                      for greedy rows the first argmax / first NaN.
-//   2. verify_decide   grid B: merges the chunks and runs the accept tests in
-//                      order with Python's min/max semantics.  A test whose
-//                      ratio lies within the normalisers' error bound of its
-//                      uniform is re-decided with exact fp64 normalisers.
-//   3. verify_residual grid (B x chunks): for a rejected position r, the
-//                      chunk masses of max(p - q, 0) (fp64).
-//   4. verify_draw     grid B: locates u * R among the chunk masses and scans
-//                      the chunk; a draw within the error bound of a step,
-//                      or R <= 0, is redone exactly in fp64.
+//   1. verify_stats   grid (rows x 32768-element chunks): one HBM read of
+//                     every target and draft row; per chunk the row max,
+//                     sum exp((x - m) / T) (fp32 exp2 terms, fp64 sums) and
+//                     the logit at the drafted token, or for greedy rows the
+//                     first argmax / first NaN.
+//   2. verify_decide  grid B: one thread per row merges its chunks, one lane
+//                     per position runs the accept test with Python's
+//                     min/max semantics; a test whose ratio lies within the
+//                     normalisers' error bound of its uniform is re-decided
+//                     with exact fp64 normalisers.
+//   3. verify_norm    one wave per 512-element sub-chunk of the row pair at
+//                     the rejected position r: exact fp64 normaliser
+//                     partials of p and q, and the residual max(p - q, 0)
+//                     split into elements whose sign is sure (summed) and the
+//                     few that are not (listed).
+//   4. verify_draw    grid B: exact normalisers, the residual mass of every
+//                     sub-chunk from the partials, the sub-chunk holding
+//                     u * R, and a scan of it; a draw within 1e-12 (relative)
+//                     of a step is redone over the whole row pair.
+//
+// fp64 terms use exp64 (table-driven, within 1 ulp) of fl32(x / T), the
+// reference's fp32 quotient (div32).
 #include "cx_device.hpp"
 #include "cx_sampler.h"
 #include "cx_internal.hpp"
@@ -43,49 +53,117 @@ __device__ __forceinline__ const float* drow(const VerifyArgs& A, int b, int i) 
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-// ------------------------------------------------------------ 1. stats
-__global__ __launch_bounds__(WG) void verify_stats(VerifyArgs A) {
-  __shared__ double red_d[2 * NWAVE + 4];
-  __shared__ int red_i[2 * NWAVE + 4];
-  const int nt = A.B * (A.gamma + 1);
-  const int r = blockIdx.x / A.nchunk;
-  const int ch = blockIdx.x % A.nchunk;
-  int b, i;
-  const float* row;
-  if (r < nt) { b = r / (A.gamma + 1); i = r % (A.gamma + 1); row = trow(A, b, i); }
-  else { b = (r - nt) / A.gamma; i = (r - nt) % A.gamma; row = drow(A, b, i); }
-  const float T = A.temperature[b];
-  const bool greedy = T == 0.0f;
-  if (greedy && r >= nt) return;                       // greedy never reads q rows
-  const int lo = ch * VCHUNK, hi = min(A.V, lo + VCHUNK);
+// Exact normaliser of softmax64(row / T): sum exp(fl32(x / T) - fl32(max x / T)).
+__device__ inline double exact_row_sum(const float* row, int V, double invT, double zm,
+                                       const double* tab, double* red_d) {
+  double s = 0.0;
+  for (int e = threadIdx.x; e < V; e += WG) s += exp64(div32(row[e], invT) - zm, tab);
+  return block_sum(s, red_d);
+}
+
+// Python's min(1.0, p / max(q, 1e-12)) (speculative.py:158).
+__device__ __forceinline__ double accept_threshold(double p, double q) {
+  double qq = 1e-12 > q ? 1e-12 : q;
+  double r = p / qq;
+  return r < 1.0 ? r : 1.0;
+}
+
+// The rejected position's row pair as the residual sees it.
+struct ResidCtx {
+  double invT;            // 1 / T
+  double zmt, zmq;        // fl32(max x / T) of the target and draft rows
+  double invSt, invSq;    // 1 / normalisers
+  const double* tab;      // EXP64_TAB in LDS
+};
+
+// Residual weight max(p - q, 0) of one element, fp64 (speculative.py:161).
+__device__ __forceinline__ double resid(float xt, float xq, const ResidCtx& C) {
+  double p = exp64(div32(xt, C.invT) - C.zmt, C.tab) * C.invSt;
+  double q = exp64(div32(xq, C.invT) - C.zmq, C.tab) * C.invSq;
+  double d = p - q;
+  return d > 0.0 ? d : 0.0;
+}
+
+// Exact residual draw over the whole row pair (single workgroup, fp64):
+// numpy's choice(V, p=r/R) with r = max(p - q, 0) (speculative.py:161-166).
+// Returns -1 when R <= 0 (the caller falls back to argmax(row)).
+__device__ inline int exact_residual_draw(const float* tr, const float* dr, int V,
+                                          const ResidCtx& C, double u, double* red_d,
+                                          int* red_i, double* tsum) {
   const int t = threadIdx.x;
-  ChunkStats* out = A.cstats + (size_t)r * A.nchunk + ch;
+  const int per = (V + WG - 1) / WG;
+  const int e0 = min(V, t * per), e1 = min(V, e0 + per);
+  double s = 0.0;
+  for (int e = e0; e < e1; ++e) s += resid(tr[e], dr[e], C);
+  tsum[t] = s;
+  const double R = block_sum(s, red_d);
+  if (!(R > 0.0)) return -1;
+  block_scan(tsum, WG, red_d);            // inclusive prefix of the per-thread sums
+  const double prev = t > 0 ? tsum[t - 1] : 0.0;
+  int found = INT_MAX;
+  if ((prev / R) / (tsum[WG - 1] / R) <= u && (tsum[t] / R) / (tsum[WG - 1] / R) > u) {
+    double run = prev;
+    for (int e = e0; e < e1; ++e) {
+      run += resid(tr[e], dr[e], C);
+      if ((run / R) / (tsum[WG - 1] / R) > u) { found = e; break; }
+    }
+  }
+  found = block_min(found, red_i, INT_MAX);
+  if (found == INT_MAX) found = V - 1;
+  return found;
+}
+
+__device__ inline int row_argmax(const float* row, int V, double* red_d, int* red_i) {
+  double bv = -__builtin_inf();
+  int bi = INT_MAX, ni = INT_MAX;
+  for (int e = threadIdx.x; e < V; e += WG) {
+    float x = row[e];
+    if (x != x) ni = min(ni, e);
+    else argmax_merge(bv, bi, (double)x, e);
+  }
+  block_argmax(bv, bi, red_d, red_i);
+  ni = block_min(ni, red_i, INT_MAX);
+  return ni != INT_MAX ? ni : (bi == INT_MAX ? 0 : bi);
+}
+
+// ------------------------------------------------------------ 1. stats
+// Chunk statistics of one row for greedy rows: first max and first NaN.
+__device__ inline void stats_greedy(const float* row, int lo, int hi, ChunkStats* out,
+                                    double* red_d, int* red_i) {
+  const int t = threadIdx.x;
   const bool vec = (((uintptr_t)row) & 15) == 0;
   const int64_t v0 = vec ? lo / 4 : 0, v1 = vec ? hi / 4 : 0;
   const f32x4* vp = (const f32x4*)row;
-  if (greedy) {
-    float bv = -__builtin_inff();
-    int bi = INT_MAX, ni = INT_MAX;
-    for (int64_t vi = v0 + t; vi < v1; vi += WG) {
-      f32x4 q = __builtin_nontemporal_load(&vp[vi]);
-      float x[4] = {q.x, q.y, q.z, q.w};
+  float bv = -__builtin_inff();
+  int bi = INT_MAX, ni = INT_MAX;
+  for (int64_t vi = v0 + t; vi < v1; vi += WG) {
+    f32x4 q = __builtin_nontemporal_load(&vp[vi]);
+    float x[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (x[j] > bv) { bv = x[j]; bi = (int)(vi * 4 + j); }
-        if (x[j] != x[j] && ni == INT_MAX) ni = (int)(vi * 4 + j);
-      }
+    for (int j = 0; j < 4; ++j) {
+      if (x[j] > bv) { bv = x[j]; bi = (int)(vi * 4 + j); }
+      if (x[j] != x[j] && ni == INT_MAX) ni = (int)(vi * 4 + j);
     }
-    for (int64_t e = (vec ? (v1 * 4 > lo ? v1 * 4 : lo) : lo) + t; e < hi; e += WG) {
-      float x = row[e];
-      if (x > bv) { bv = x; bi = (int)e; }
-      if (x != x && ni == INT_MAX) ni = (int)e;
-    }
-    double dv = bi == INT_MAX ? -__builtin_inf() : (double)bv;
-    block_argmax(dv, bi, red_d, red_i);
-    ni = block_min(ni, red_i, INT_MAX);
-    if (t == 0) { out->bv = (float)dv; out->bi = bi; out->nan_i = ni; out->m = 0; out->s = 0; }
-    return;
   }
+  for (int64_t e = (vec ? (v1 * 4 > lo ? v1 * 4 : lo) : lo) + t; e < hi; e += WG) {
+    float x = row[e];
+    if (x > bv) { bv = x; bi = (int)e; }
+    if (x != x && ni == INT_MAX) ni = (int)e;
+  }
+  double dv = bi == INT_MAX ? -__builtin_inf() : (double)bv;
+  block_argmax(dv, bi, red_d, red_i);
+  ni = block_min(ni, red_i, INT_MAX);
+  if (t == 0) { out->bv = (float)dv; out->bi = bi; out->nan_i = ni; out->m = 0; out->s = 0; }
+}
+
+// Chunk statistics of one row for stochastic rows: max of x and
+// sum exp2((x - max) * c), c = log2(e) / T.
+__device__ inline void stats_stoch(const float* row, int lo, int hi, float T, ChunkStats* out,
+                                   double* red_d) {
+  const int t = threadIdx.x;
+  const bool vec = (((uintptr_t)row) & 15) == 0;
+  const int64_t v0 = vec ? lo / 4 : 0, v1 = vec ? hi / 4 : 0;
+  const f32x4* vp = (const f32x4*)row;
   const float c = (float)(1.4426950408889634 / (double)T);
   float m = -__builtin_inff();
   double s = 0.0;
@@ -125,285 +203,462 @@ __global__ __launch_bounds__(WG) void verify_stats(VerifyArgs A) {
   if (t == 0) { out->m = M; out->s = S; out->bi = INT_MAX; out->nan_i = INT_MAX; out->bv = 0; }
 }
 
-// Merge a row's chunk statistics: max of x and sum exp((x - max) / T).
-__device__ inline void merge_row(const VerifyArgs& A, int r, float T, float& M, double& S) {
+__global__ __launch_bounds__(WG) void verify_stats(VerifyArgs A) {
+  __shared__ double red_d[2 * NWAVE + 4];
+  __shared__ int red_i[2 * NWAVE + 4];
+  const int g = A.gamma;
+  const int nt = A.B * (g + 1);
+  const int r = blockIdx.x / A.nchunk;
+  const int ch = blockIdx.x % A.nchunk;
+  int b, i;
+  const float* row;
+  bool target;
+  if (r < nt) { b = r / (g + 1); i = r % (g + 1); row = trow(A, b, i); target = true; }
+  else { b = (r - nt) / g; i = (r - nt) % g; row = drow(A, b, i); target = false; }
+  const float T = A.temperature[b];
+  const bool greedy = T == 0.0f;
+  if (greedy && !target) return;                     // greedy never reads q rows
+  const int lo = ch * VCHUNK, hi = min(A.V, lo + VCHUNK);
+  ChunkStats* out = A.cstats + (size_t)r * A.nchunk + ch;
+  if (greedy) stats_greedy(row, lo, hi, out, red_d, red_i);
+  else stats_stoch(row, lo, hi, T, out, red_d);
+  if (threadIdx.x == 0) {
+    const int tok = i < g ? A.draft_ids[(size_t)b * g + i] : -1;
+    const bool here = tok >= lo && tok < hi;
+    out->has_xt = here ? 1 : 0;
+    out->xt = here ? row[tok] : 0.0f;
+  }
+}
+
+// ------------------------------------------------------------ 2. decide
+constexpr int MERGE_GROUP = 8;          // chunk statistics loaded at once per row
+
+// Merge the chunk statistics of stochastic row r: max of x, sum
+// exp((x - max) / T) and the logit at the drafted token.
+__device__ inline void merge_row(const VerifyArgs& A, int r, float T, float& M, double& S,
+                                 float& xt) {
   const ChunkStats* cs = A.cstats + (size_t)r * A.nchunk;
   const double c = (double)(float)(1.4426950408889634 / (double)T);
   M = -__builtin_inff();
-  for (int k = 0; k < A.nchunk; ++k) M = fmaxf(M, cs[k].m);
   S = 0.0;
+  xt = 0.0f;
   bool nan = false;
-  for (int k = 0; k < A.nchunk; ++k) {
-    nan |= cs[k].s != cs[k].s;
-    if (cs[k].s != 0.0) S += cs[k].s * exp2((double)(cs[k].m - M) * c);
+  for (int k0 = 0; k0 < A.nchunk; k0 += MERGE_GROUP) {
+    float m[MERGE_GROUP];
+    double s[MERGE_GROUP];
+#pragma unroll
+    for (int j = 0; j < MERGE_GROUP; ++j) {
+      const bool in = k0 + j < A.nchunk;
+      m[j] = in ? cs[k0 + j].m : -__builtin_inff();
+      s[j] = in ? cs[k0 + j].s : 0.0;
+      if (in && cs[k0 + j].has_xt) xt = cs[k0 + j].xt;
+    }
+    float gm = M;
+#pragma unroll
+    for (int j = 0; j < MERGE_GROUP; ++j) gm = fmaxf(gm, m[j]);
+    if (S != 0.0) S *= exp2((double)(M - gm) * c);
+    M = gm;
+#pragma unroll
+    for (int j = 0; j < MERGE_GROUP; ++j) {
+      nan |= s[j] != s[j];
+      if (s[j] != 0.0) S += s[j] * exp2((double)(m[j] - M) * c);
+    }
   }
   if (nan) S = __builtin_nan("");
 }
 
-// Exact normaliser of softmax64(row / T): sum exp(f64(x / T) - f64(max(x) / T)).
-__device__ inline double exact_row_sum(const float* row, int V, float T, float zm,
-                                       double* red_d) {
-  double s = 0.0;
-  for (int e = threadIdx.x; e < V; e += WG) s += exp((double)(row[e] / T) - (double)zm);
-  return block_sum(s, red_d);
+// First maximum / first NaN of greedy row r from its chunk statistics.
+__device__ inline int merge_greedy(const VerifyArgs& A, int r) {
+  const ChunkStats* cs = A.cstats + (size_t)r * A.nchunk;
+  double bv = -__builtin_inf();
+  int bi = INT_MAX, ni = INT_MAX;
+  for (int k0 = 0; k0 < A.nchunk; k0 += MERGE_GROUP) {
+    float v[MERGE_GROUP];
+    int i[MERGE_GROUP], n[MERGE_GROUP];
+#pragma unroll
+    for (int j = 0; j < MERGE_GROUP; ++j) {
+      const bool in = k0 + j < A.nchunk;
+      v[j] = in ? cs[k0 + j].bv : 0.0f;
+      i[j] = in ? cs[k0 + j].bi : INT_MAX;
+      n[j] = in ? cs[k0 + j].nan_i : INT_MAX;
+    }
+#pragma unroll
+    for (int j = 0; j < MERGE_GROUP; ++j) {
+      if (i[j] != INT_MAX) argmax_merge(bv, bi, (double)v[j], i[j]);
+      ni = min(ni, n[j]);
+    }
+  }
+  return ni != INT_MAX ? ni : (bi == INT_MAX ? 0 : bi);
 }
 
-// Python's min(1.0, p / max(q, 1e-12)) (speculative.py:158).
-__device__ __forceinline__ double accept_threshold(double p, double q) {
-  double qq = 1e-12 > q ? 1e-12 : q;
-  double r = p / qq;
-  return r < 1.0 ? r : 1.0;
-}
-
-// ------------------------------------------------------------ 2. decide
 __global__ __launch_bounds__(WG) void verify_decide(VerifyArgs A) {
   __shared__ double red_d[2 * NWAVE + 4];
-  __shared__ int s_verdict;
+  __shared__ int red_i[2 * NWAVE + 4];
+  __shared__ double tab[64];
+  __shared__ float s_M[2 * GAMMA_MAX + 1];
+  __shared__ double s_S[2 * GAMMA_MAX + 1];
+  __shared__ float s_x[2 * GAMMA_MAX + 1];
+  __shared__ int s_best[GAMMA_MAX + 1];
+  __shared__ int s_f, s_kind;
+  load_exp64_tab(tab);
   const int b = blockIdx.x;
-  const int t = threadIdx.x;
   const int g = A.gamma;
+  const int t = threadIdx.x;
   const float T = A.temperature[b];
-  SeqState* sq = A.seq + b;
   const int nt = A.B * (g + 1);
+  const int32_t* ids = A.draft_ids + (size_t)b * g;
+  SeqState out;
+  out.accepted = 0; out.next_tok = -1; out.used = 0; out.status = 0;
+  out.rej1 = 0; out.exact = 0; out.Mt = 0.f; out.Mq = 0.f;
+  out.St = 0.0; out.Sq = 0.0; out.R = 0.0; out.pad = 0.0;
   if (T == 0.0f) {                                    // speculative.py:150-155
+    for (int i = t; i <= g; i += WG) s_best[i] = merge_greedy(A, b * (g + 1) + i);
+    __syncthreads();
     if (t == 0) {
-      int acc = 0, nxt = -1;
-      for (int i = 0; i <= g; ++i) {
-        const ChunkStats* cs = A.cstats + ((size_t)b * (g + 1) + i) * A.nchunk;
-        double bv = -__builtin_inf();
-        int bi = INT_MAX, ni = INT_MAX;
-        for (int k = 0; k < A.nchunk; ++k) {
-          if (cs[k].bi != INT_MAX) argmax_merge(bv, bi, (double)cs[k].bv, cs[k].bi);
-          ni = min(ni, cs[k].nan_i);
-        }
-        int best = ni != INT_MAX ? ni : (bi == INT_MAX ? 0 : bi);
-        if (i == g || A.draft_ids[(size_t)b * g + i] != best) { nxt = best; break; }
-        ++acc;
-      }
+      int acc = 0;
+      while (acc < g && ids[acc] == s_best[acc]) ++acc;
       A.accepted[b] = acc;
-      A.next_tok[b] = nxt;
+      A.next_tok[b] = s_best[acc];                    // row gamma: the bonus token
       A.used[b] = 0;
       A.row_status[b] = CX_ROW_GREEDY;
-      sq->rej = -1;
+      A.seq[b] = out;
     }
     return;
   }
-  // ids outside [0, V) or a missing draft tensor cannot be verified: report
-  // the sequence as unsupported without touching any row.
-  bool bad = A.draft == nullptr;
-  for (int k = 0; k < g; ++k) {
-    const int id = A.draft_ids[(size_t)b * g + k];
-    bad |= id < 0 || id >= A.V;
-  }
+  // ids outside [0, V) or missing draft rows cannot be verified: report the
+  // sequence as unsupported
+  int bad = (A.draft == nullptr || !A.draft_rows) ? 1 : 0;
+  for (int k = t; k < g; k += WG) bad |= (ids[k] < 0 || ids[k] >= A.V) ? 1 : 0;
+  bad = block_max(bad, red_i, 0);
   if (bad) {
     if (t == 0) {
-      sq->rej = -1;
       A.accepted[b] = 0; A.next_tok[b] = -1; A.used[b] = 0;
       A.row_status[b] = CX_ROW_UNSUPPORTED;
+      A.seq[b] = out;
     }
     return;
   }
+  // one thread per row: target rows 0..g-1 at [0, g), draft rows at [g, 2g)
+  for (int j = t; j < 2 * g; j += WG) {
+    const int r = j < g ? b * (g + 1) + j : nt + b * g + (j - g);
+    float M, xt;
+    double S;
+    merge_row(A, r, T, M, S, xt);
+    s_M[j] = M; s_S[j] = S; s_x[j] = xt;
+  }
+  __syncthreads();
   const double* ub = A.u + (size_t)b * (g + 1);
-  int i = 0;
-  for (; i < g; ++i) {
-    const int tok = A.draft_ids[(size_t)b * g + i];
-    const float* tr = trow(A, b, i);
-    const float* dr = drow(A, b, i);
-    float Mt, Mq;
-    double St, Sq;
-    merge_row(A, b * (g + 1) + i, T, Mt, St);
-    merge_row(A, nt + b * g + i, T, Mq, Sq);
-    const float zmt = Mt / T, zmq = Mq / T;
-    const double et = exp((double)(tr[tok] / T) - (double)zmt);
-    const double eq = exp((double)(dr[tok] / T) - (double)zmq);
-    double thr = accept_threshold(et / St, eq / Sq);
-    const double ui = ub[i];
-    bool exact = false;
+  const double invT = 1.0 / (double)T;
+  int start = 0, rej = -1;
+  bool exact = false;
+  double St = 0.0, Sq = 0.0;
+  for (;;) {
+    // first position at or after `start` that rejects, or whose test lies
+    // within the error bound of its uniform (speculative.py:156-160)
+    if (t < 64) {
+      int f = -1;
+      for (int base = start; base < g && f < 0; base += 64) {
+        const int i = base + t;
+        bool rj = false, nr = false;
+        if (i < g) {
+          const float zmt = s_M[i] / T, zmq = s_M[g + i] / T;
+          const double st = s_S[i], sqq = s_S[g + i];
+          const double et = exp64(div32(s_x[i], invT) - (double)zmt, tab);
+          const double eq = exp64(div32(s_x[g + i], invT) - (double)zmq, tab);
+          const double thr = accept_threshold(et / st, eq / sqq);
+          const double ui = ub[i];
+          const double rel = 2.0 * (tol_norm(zmt) + tol_norm(zmq));
+          const double tol = rel * (thr == thr ? thr : 1.0) + 1e-300;
+          const bool q_floor_near = fabs(eq / sqq - 1e-12) <= rel * 1e-12;
+          nr = st == st && sqq == sqq && (fabs(ui - thr) <= tol || q_floor_near);
+          rj = !(ui < thr);
+        }
+        const uint64_t m = __ballot(rj || nr);
+        if (m) {
+          const int fl = __builtin_ctzll(m);
+          f = base + fl;
+          if (t == fl) { s_f = f; s_kind = nr ? 2 : 1; }
+        }
+      }
+      if (t == 0 && f < 0) { s_f = g; s_kind = 0; }
+    }
+    __syncthreads();
+    const int f = s_f, kind = s_kind;
+    __syncthreads();
+    if (kind == 0) break;                              // every test accepts
+    St = s_S[f];
+    Sq = s_S[g + f];
+    if (kind == 1) { rej = f; break; }
     // near the decision: recompute both normalisers exactly (fp64 over the rows)
-    const double rel = 2.0 * (tol_norm(zmt) + tol_norm(zmq));
-    const double tol = rel * (thr == thr ? thr : 1.0) + 1e-300;
-    const bool q_floor_near = fabs(eq / Sq - 1e-12) <= rel * 1e-12;
-    if (St == St && Sq == Sq && (fabs(ui - thr) <= tol || q_floor_near)) {
-      St = exact_row_sum(tr, A.V, T, zmt, red_d);
-      Sq = exact_row_sum(dr, A.V, T, zmq, red_d);
-      thr = accept_threshold(et / St, eq / Sq);
-      exact = true;
-    }
-    if (ui < thr) continue;
-    if (t == 0) {
-      sq->rej = i; sq->Mt = Mt; sq->Mq = Mq; sq->St = St; sq->Sq = Sq; sq->exact = exact;
-    }
-    break;
+    const float zmt = s_M[f] / T, zmq = s_M[g + f] / T;
+    St = exact_row_sum(trow(A, b, f), A.V, invT, (double)zmt, tab, red_d);
+    Sq = exact_row_sum(drow(A, b, f), A.V, invT, (double)zmq, tab, red_d);
+    const double et = exp64(div32(s_x[f], invT) - (double)zmt, tab);
+    const double eq = exp64(div32(s_x[g + f], invT) - (double)zmq, tab);
+    if (!(ub[f] < accept_threshold(et / St, eq / Sq))) { rej = f; exact = true; break; }
+    start = f + 1;
   }
   if (t == 0) {
-    A.accepted[b] = i;
-    if (i == g) {                                     // speculative.py:168-171
-      sq->rej = -1;
+    if (rej < 0) {                                    // speculative.py:168-171
+      A.accepted[b] = g;
       A.next_tok[b] = -1;
       A.used[b] = g;
       A.row_status[b] = CX_ROW_OK;
     } else {
-      A.used[b] = i + 2;                              // tests 0..i, then the residual draw
+      out.rej1 = rej + 1;
+      out.Mt = s_M[rej];
+      out.Mq = s_M[g + rej];
+      out.St = St;
+      out.Sq = Sq;
+      out.exact = exact;
+      A.accepted[b] = rej;
+      A.used[b] = rej + 2;                            // tests 0..rej, then the residual draw
     }
+    A.seq[b] = out;
   }
 }
 
-// Residual weight of element e at position (b, rej): max(p - q, 0) in fp64.
-__device__ __forceinline__ double resid(float xt, float xq, float T, float zmt, float zmq,
-                                        double invSt, double invSq) {
-  double p = exp((double)(xt / T) - (double)zmt) * invSt;
-  double q = exp((double)(xq / T) - (double)zmq) * invSq;
-  double d = p - q;
-  return d > 0.0 ? d : 0.0;
+// ------------------------------------------------------------ 3. normaliser partials
+// The margin around lam0 inside which a residual sign is not yet known:
+// well above the error of the fp32-term normalisers behind lam0, or tiny
+// when lam0 came from exact ones.
+__device__ __forceinline__ double sign_margin(const SeqState& q, float T) {
+  if (q.exact) return 1e-9;
+  const double m = 20.0 * (tol_norm(q.Mt / T) + tol_norm(q.Mq / T));
+  return m > 1e-3 ? m : 1e-3;
 }
 
-// ------------------------------------------------------------ 3. residual chunk masses
-__global__ __launch_bounds__(WG) void verify_residual(VerifyArgs A) {
-  __shared__ double red_d[2 * NWAVE + 4];
-  const int b = blockIdx.x / A.nchunk, ch = blockIdx.x % A.nchunk;
+// Eight consecutive logits [e0, e0 + 8) of a row (zeros past hi), with two
+// 16-byte loads when they are whole and aligned.
+__device__ __forceinline__ void load8(const float* row, int e0, int hi, float (&x)[8]) {
+  if (e0 + 8 <= hi && (((uintptr_t)(row + e0)) & 15) == 0) {
+    const f32x4 a = __builtin_nontemporal_load((const f32x4*)(row + e0));
+    const f32x4 c = __builtin_nontemporal_load((const f32x4*)(row + e0) + 1);
+    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+    x[4] = c.x; x[5] = c.y; x[6] = c.z; x[7] = c.w;
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = e0 + j < hi ? row[e0 + j] : 0.0f;
+  }
+}
+
+static_assert(SUB == 64 * 8, "a normaliser partial is one wave of 8 elements per lane");
+
+// One wave per 512-element sub-chunk of the rejected row pair.
+__global__ __launch_bounds__(WG) void verify_norm(VerifyArgs A) {
+  __shared__ double tab[64];
+  const int per_b = (A.nsub + NWAVE - 1) / NWAVE;
+  const int b = blockIdx.x / per_b;
   const float T = A.temperature[b];
-  const SeqState* sq = A.seq + b;
-  if (T == 0.0f || sq->rej < 0) return;
-  const int r = sq->rej;
+  const SeqState q = A.seq[b];
+  if (T == 0.0f || q.rej1 == 0) return;
+  load_exp64_tab(tab);
+  const int sub = (blockIdx.x % per_b) * NWAVE + wave_id();
+  if (sub >= A.nsub) return;
+  const int r = q.rej1 - 1;
   const float* tr = trow(A, b, r);
   const float* dr = drow(A, b, r);
-  const float zmt = sq->Mt / T, zmq = sq->Mq / T;
-  const double it = 1.0 / sq->St, iq = 1.0 / sq->Sq;
-  const int lo = ch * VCHUNK, hi = min(A.V, lo + VCHUNK);
-  double s = 0.0;
-  for (int e = lo + threadIdx.x; e < hi; e += WG) s += resid(tr[e], dr[e], T, zmt, zmq, it, iq);
-  s = block_sum(s, red_d);
-  if (threadIdx.x == 0) A.rmass[(size_t)b * A.nchunk + ch] = s;
-}
-
-// Exact residual draw over the whole row pair (single workgroup, fp64):
-// numpy's choice(V, p=r/R) with r = max(p - q, 0) (speculative.py:161-166).
-// Returns -1 when R <= 0 (the caller falls back to argmax(row)).
-__device__ inline int exact_residual_draw(const float* tr, const float* dr, int V, float T,
-                                          float zmt, float zmq, double St, double Sq, double u,
-                                          double* red_d, int* red_i, double* tsum) {
-  const int t = threadIdx.x;
-  const int per = (V + WG - 1) / WG;
-  const int e0 = t * per, e1 = min(V, e0 + per);
-  const double it = 1.0 / St, iq = 1.0 / Sq;
-  double s = 0.0;
-  for (int e = e0; e < e1; ++e) s += resid(tr[e], dr[e], T, zmt, zmq, it, iq);
-  tsum[t] = s;
-  const double R = block_sum(s, red_d);
-  if (!(R > 0.0)) return -1;
-  block_scan(tsum, WG, red_d);            // inclusive prefix of the per-thread sums
-  const double prev = t > 0 ? tsum[t - 1] : 0.0;
-  int found = INT_MAX;
-  if ((prev / R) / (tsum[WG - 1] / R) <= u && (tsum[t] / R) / (tsum[WG - 1] / R) > u) {
-    double run = prev;
-    for (int e = e0; e < e1; ++e) {
-      run += resid(tr[e], dr[e], T, zmt, zmq, it, iq);
-      if ((run / R) / (tsum[WG - 1] / R) > u) { found = e; break; }
+  const double zmt = q.Mt / T, zmq = q.Mq / T;
+  const double invT = 1.0 / (double)T;
+  const double lam0 = q.St / q.Sq;
+  const double eps = sign_margin(q, T);
+  const int l = lane_id();
+  const int e0 = sub * SUB + l * 8;
+  float xt[8], xq[8];
+  load8(tr, e0, A.V, xt);
+  load8(dr, e0, A.V, xq);
+  double ev[8], fv[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {                       // branch-free: the exps interleave
+    const bool in = e0 + j < A.V;
+    ev[j] = in ? exp64(div32(xt[j], invT) - zmt, tab) : 0.0;
+    fv[j] = in ? exp64(div32(xq[j], invT) - zmq, tab) : 0.0;
+  }
+  double se = 0.0, sf = 0.0, dp = 0.0, fp = 0.0;
+  unsigned amb = 0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const double e = ev[j], f = fv[j];
+    se += e;
+    sf += f;
+    const double lf = lam0 * f;
+    const bool pos = e > lf * (1.0 + eps);
+    dp += pos ? e - lf : 0.0;
+    fp += pos ? f : 0.0;
+    amb |= (!pos && e >= lf * (1.0 - eps) && (e != 0.0 || f != 0.0)) ? 1u << j : 0u;
+  }
+  se = wave_reduce(se, OpAdd());
+  sf = wave_reduce(sf, OpAdd());
+  dp = wave_reduce(dp, OpAdd());
+  fp = wave_reduce(fp, OpAdd());
+  const size_t part = (size_t)b * A.nsub + sub;
+  int namb = 0;
+  if (__ballot(amb != 0)) {                           // rare: list the undecided signs
+    AmbEntry* out = A.amb + part * AMB_CAP;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const bool a = (amb >> j) & 1u;
+      const uint64_t m = __ballot(a);
+      const int idx = namb + lanes_below(m);
+      if (a && idx < AMB_CAP) { out[idx].e = ev[j]; out[idx].f = fv[j]; }
+      namb += __builtin_popcountll(m);
     }
   }
-  found = block_min(found, red_i, INT_MAX);
-  if (found == INT_MAX) found = V - 1;
-  return found;
-}
-
-__device__ inline int row_argmax(const float* row, int V, double* red_d, int* red_i) {
-  double bv = -__builtin_inf();
-  int bi = INT_MAX, ni = INT_MAX;
-  for (int e = threadIdx.x; e < V; e += WG) {
-    float x = row[e];
-    if (x != x) ni = min(ni, e);
-    else argmax_merge(bv, bi, (double)x, e);
+  if (l == 0) {
+    NormPart P;
+    P.se = se; P.sf = sf; P.dp = dp; P.fp = fp;
+    P.namb = namb;
+    for (int k = 0; k < 7; ++k) P.pad[k] = 0;
+    A.npart[part] = P;
   }
-  block_argmax(bv, bi, red_d, red_i);
-  ni = block_min(ni, red_i, INT_MAX);
-  return ni != INT_MAX ? ni : (bi == INT_MAX ? 0 : bi);
 }
 
 // ------------------------------------------------------------ 4. draw
+// numpy's choice(V, p=r/R) with r = max(p - q, 0) (speculative.py:161-166).
+// With e, f the exp terms of the rejected row pair, St, Sq their exact sums
+// and lam = St / Sq, r = St^-1 w with w = max(e - lam f, 0): the draw runs on
+// w and W = sum w.
 __global__ __launch_bounds__(WG) void verify_draw(VerifyArgs A) {
   __shared__ double red_d[2 * NWAVE + 4];
   __shared__ int red_i[2 * NWAVE + 4];
-  __shared__ double tsum[WG];
-  __shared__ double cm[64];
-  __shared__ int s_ch;
+  __shared__ double tab[64];
+  __shared__ double tsum[2 * WG];
+  __shared__ int s_over[64];
+  __shared__ int s_nover;
   const int b = blockIdx.x;
   const int t = threadIdx.x;
   const float T = A.temperature[b];
-  SeqState* sq = A.seq + b;
-  if (T == 0.0f || sq->rej < 0) return;
-  const int r = sq->rej;
+  const SeqState q = A.seq[b];
+  if (T == 0.0f || q.rej1 == 0) return;
+  load_exp64_tab(tab);
+  const int r = q.rej1 - 1;
   const int g = A.gamma;
+  const int ns = A.nsub;                              // <= 2 * WG
   const float* tr = trow(A, b, r);
   const float* dr = drow(A, b, r);
-  const float zmt = sq->Mt / T, zmq = sq->Mq / T;
   const double u = A.u[(size_t)b * (g + 1) + r + 1];
-  const double* rm = A.rmass + (size_t)b * A.nchunk;
-  int tok = -1;
-  int flag = 0;
-  double R = 0.0;
-  for (int k = 0; k < A.nchunk; ++k) R += rm[k];
-  // error of the fp32-term normalisers carries into every p and q
-  const double err = sq->exact ? 1e-12 : 2.0 * (tol_norm(zmt) + tol_norm(zmq));
-  bool ok = R > err;
-  if (ok) {
-    if (t == 0) {
-      double run = 0.0;
-      int k = 0;
-      for (; k < A.nchunk - 1; ++k) {
-        if ((run + rm[k]) / R > u) break;
-        run += rm[k];
-      }
-      s_ch = k;
-      cm[0] = run;
-      // distance of u*R to the chunk's edges, relative to R
-      double lo_gap = u - run / R, hi_gap = (run + rm[k]) / R - u;
-      cm[1] = fmin(k > 0 ? lo_gap : 1.0, k < A.nchunk - 1 ? hi_gap : 1.0);
-    }
-    __syncthreads();
-    const int k = s_ch;
-    const double before = cm[0];
-    if (cm[1] <= err / R) ok = false;
-    if (ok) {
-      const int lo = k * VCHUNK, hi = min(A.V, lo + VCHUNK);
-      const int per = (hi - lo + WG - 1) / WG;
-      const int e0 = lo + t * per, e1 = min(hi, e0 + per);
-      const double it = 1.0 / sq->St, iq = 1.0 / sq->Sq;
-      double s = 0.0;
-      for (int e = e0; e < e1; ++e) s += resid(tr[e], dr[e], T, zmt, zmq, it, iq);
-      tsum[t] = s;
-      __syncthreads();
-      block_scan(tsum, WG, red_d);
-      const double prev = before + (t > 0 ? tsum[t - 1] : 0.0);
-      int found = INT_MAX;
-      double margin = 1.0;
-      if (prev / R <= u && (before + tsum[t]) / R > u) {
-        double run = prev;
-        for (int e = e0; e < e1; ++e) {
-          double nx = run + resid(tr[e], dr[e], T, zmt, zmq, it, iq);
-          if (nx / R > u) { found = e; margin = fmin(u - run / R, nx / R - u); break; }
-          run = nx;
+  const NormPart* np = A.npart + (size_t)b * ns;
+  // this thread's sub-chunks 2t and 2t + 1
+  NormPart P[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int sidx = 2 * t + k;
+    if (sidx < ns) P[k] = np[sidx];
+    else { P[k].se = P[k].sf = P[k].dp = P[k].fp = 0.0; P[k].namb = 0; }
+  }
+  if (t == 0) s_nover = 0;
+  // exact normalisers (fixed reduction order)
+  const double St = block_sum(P[0].se + P[1].se, red_d);
+  const double Sq = block_sum(P[0].sf + P[1].sf, red_d);
+  const double lam = St / Sq, lam0 = q.St / q.Sq;
+  ResidCtx C;
+  C.invT = 1.0 / (double)T;
+  C.zmt = q.Mt / T;
+  C.zmq = q.Mq / T;
+  C.invSt = 1.0 / St;
+  C.invSq = 1.0 / Sq;
+  C.tab = tab;
+  // residual mass of each sub-chunk: the sure-positive part and the list
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int sidx = 2 * t + k;
+    double w = 0.0;
+    if (sidx < ns) {
+      if (P[k].namb > AMB_CAP) {
+        const int o = atomicAdd(&s_nover, 1);
+        if (o < 64) s_over[o] = sidx;
+      } else {
+        w = P[k].dp - (lam - lam0) * P[k].fp;
+        const AmbEntry* am = A.amb + ((size_t)b * ns + sidx) * AMB_CAP;
+        for (int j = 0; j < P[k].namb; ++j) {
+          const double d = am[j].e - lam * am[j].f;
+          w += d > 0.0 ? d : 0.0;
         }
       }
-      found = block_min(found, red_i, INT_MAX);
+    }
+    if (sidx < ns) tsum[sidx] = w;
+  }
+  __syncthreads();
+  const int nover = s_nover;
+  bool ok = nover <= 64;
+  for (int o = 0; o < nover && o < 64; ++o) {         // lists that overflowed: direct sums
+    const int sidx = s_over[o];
+    const int e = sidx * SUB + t;
+    double d = 0.0;
+    if (t < SUB && e < A.V)
+      d = exp64(div32(tr[e], C.invT) - C.zmt, tab) - lam * exp64(div32(dr[e], C.invT) - C.zmq, tab);
+    d = block_sum(d > 0.0 ? d : 0.0, red_d);
+    if (t == 0) tsum[sidx] = d;
+    __syncthreads();
+  }
+  block_scan(tsum, ns, red_d);                        // inclusive prefix over sub-chunks
+  const double W = tsum[ns - 1];
+  if (W != W || St != St || Sq != Sq) {              // NaN probabilities: numpy raises
+    if (t == 0) {
+      A.next_tok[b] = -1;
+      A.used[b] = r + 1;
+      A.row_status[b] = CX_ROW_ERROR;
+    }
+    return;
+  }
+  const double err = 1e-12;                           // relative rounding of the sums
+  ok = ok && W > err * St;
+  int tok = -1, flag = 0;
+  if (ok) {
+    // the sub-chunk holding u * W, and u's distance to its edges
+    int found = INT_MAX;
+    double gap = 1.0;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int sidx = 2 * t + k;
+      if (sidx >= ns) continue;
+      const double lo = sidx > 0 ? tsum[sidx - 1] / W : 0.0, hi = tsum[sidx] / W;
+      if (lo <= u && u < hi) {
+        found = sidx;
+        gap = fmin(sidx > 0 ? u - lo : 1.0, sidx < ns - 1 ? hi - u : 1.0);
+      }
+    }
+    found = block_min(found, red_i, INT_MAX);
+    gap = block_min(gap, red_d, 1.0);
+    if (found == INT_MAX || gap <= err) ok = false;
+    if (ok) {
+      const double before = found > 0 ? tsum[found - 1] : 0.0;
+      __syncthreads();                                // tsum is reused below
+      const int e = found * SUB + t;
+      double w = 0.0;
+      if (t < SUB && e < A.V) {
+        const double d = exp64(div32(tr[e], C.invT) - C.zmt, tab) -
+                         lam * exp64(div32(dr[e], C.invT) - C.zmq, tab);
+        w = d > 0.0 ? d : 0.0;
+      }
+      if (t < SUB) tsum[t] = w;
+      __syncthreads();
+      block_scan(tsum, SUB, red_d);
+      int hit = INT_MAX;
+      double margin = 1.0;
+      if (t < SUB && e < A.V) {
+        const double lo = (before + (t > 0 ? tsum[t - 1] : 0.0)) / W;
+        const double hi = (before + tsum[t]) / W;
+        if (lo <= u && u < hi) { hit = e; margin = fmin(u - lo, hi - u); }
+      }
+      hit = block_min(hit, red_i, INT_MAX);
       margin = block_min(margin, red_d, 1.0);
-      if (found == INT_MAX || margin <= err / R) ok = false;
-      else tok = found;
+      if (hit == INT_MAX || margin <= err) ok = false;
+      else tok = hit;
     }
   }
-  if (!ok) {                                            // exact fp64 redo
-    double St = exact_row_sum(tr, A.V, T, zmt, red_d);
-    double Sq = exact_row_sum(dr, A.V, T, zmq, red_d);
+  if (!ok) {                                          // exact fp64 redo over the row pair
     __syncthreads();
-    tok = exact_residual_draw(tr, dr, A.V, T, zmt, zmq, St, Sq, u, red_d, red_i, tsum);
+    tok = exact_residual_draw(tr, dr, A.V, C, u, red_d, red_i, tsum);
     flag = CX_ROW_FLAG_EXACT;
-    if (tok < 0) {                                      // R <= 0: argmax(row), no draw
+    if (tok < 0) {                                    // R <= 0: argmax(row), no draw
       tok = row_argmax(tr, A.V, red_d, red_i);
       if (t == 0) A.used[b] = r + 1;
     }
   }
   if (t == 0) {
     A.next_tok[b] = tok;
-    A.row_status[b] = CX_ROW_OK | flag | (sq->exact ? CX_ROW_FLAG_EXACT : 0);
+    A.row_status[b] = CX_ROW_OK | flag;
   }
 }
 
@@ -413,7 +668,8 @@ int launch_verify(const VerifyArgs& A, bool any_stochastic, hipStream_t s) {
   timed_launch(CX_KERNEL_VERIFY_STATS, verify_stats, dim3(nrows * A.nchunk), dim3(WG), 0, s, A);
   timed_launch(CX_KERNEL_VERIFY_REST, verify_decide, dim3(A.B), dim3(WG), 0, s, A);
   if (any_stochastic) {
-    timed_launch(CX_KERNEL_VERIFY_REST, verify_residual, dim3(A.B * A.nchunk), dim3(WG), 0, s, A);
+    const int per_b = (A.nsub + NWAVE - 1) / NWAVE;
+    timed_launch(CX_KERNEL_VERIFY_REST, verify_norm, dim3(A.B * per_b), dim3(WG), 0, s, A);
     timed_launch(CX_KERNEL_VERIFY_REST, verify_draw, dim3(A.B), dim3(WG), 0, s, A);
   }
   return (int)hipGetLastError();
