@@ -98,12 +98,20 @@ template <int N> __device__ __forceinline__ double dpp_ror(double v) {
   const uint32_t lo = dpp_ror<N>((uint32_t)b), hi = dpp_ror<N>((uint32_t)(b >> 32));
   return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
 }
+template <int N> __device__ __forceinline__ uint64_t dpp_ror(uint64_t v) {
+  const uint32_t lo = dpp_ror<N>((uint32_t)v), hi = dpp_ror<N>((uint32_t)(v >> 32));
+  return ((uint64_t)hi << 32) | lo;
+}
 __device__ __forceinline__ uint32_t lane_read(uint32_t v, int l) {
   return (uint32_t)__builtin_amdgcn_readlane((int)v, l);
 }
 __device__ __forceinline__ int lane_read(int v, int l) { return __builtin_amdgcn_readlane(v, l); }
 __device__ __forceinline__ float lane_read(float v, int l) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+__device__ __forceinline__ uint64_t lane_read(uint64_t v, int l) {
+  const uint32_t lo = lane_read((uint32_t)v, l), hi = lane_read((uint32_t)(v >> 32), l);
+  return ((uint64_t)hi << 32) | lo;
 }
 __device__ __forceinline__ double lane_read(double v, int l) {
   const uint64_t b = (uint64_t)__double_as_longlong(v);
@@ -436,6 +444,21 @@ __device__ __forceinline__ double exp64(double x, const double* tab) {
   const double t = tab[k & 63];
   const double v = __builtin_ldexp(__builtin_fma(t, p, t), k >> 6);
   return x > -745.2 ? v : (x != x ? x : 0.0);
+}
+
+// exp(x) for x <= 0 (or -inf), as exp64 without its upper clamp and final
+// selects: x below -745.2 gives at most the smallest subnormal instead of 0,
+// which no sum of these terms can see.
+__device__ __forceinline__ double exp64_neg(double x, const double* tab) {
+  const double xc = __builtin_fmax(x, -745.2);
+  const double kd = __builtin_rint(xc * 92.33248261689366);
+  double r = __builtin_fma(-kd, 0.010830424696223417, xc);
+  r = __builtin_fma(-kd, 2.572804622327669e-14, r);
+  const int k = (int)kd;
+  const double p = r * __builtin_fma(r, __builtin_fma(r, __builtin_fma(r, __builtin_fma(
+                           r, 1.0 / 120.0, 1.0 / 24.0), 1.0 / 6.0), 0.5), 1.0);
+  const double t = tab[k & 63];
+  return __builtin_ldexp(__builtin_fma(t, p, t), k >> 6);
 }
 
 // fl32(x / T) for fp32 x and T, given invT = 1 / (double)T: the fp64 product

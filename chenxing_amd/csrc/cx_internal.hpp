@@ -79,7 +79,7 @@ struct SampleArgs {
 };
 
 // ---------------------------------------------------------------- verify
-constexpr int VCHUNK = 32768;          // elements per verify stats chunk
+constexpr int VCHUNK = 2048;           // elements per verify stats partial: one wave, 32 per lane
 constexpr int GAMMA_MAX = 256;         // longest draft the verify kernels accept
 
 struct ChunkStats {                    // 32 bytes per (row, chunk)

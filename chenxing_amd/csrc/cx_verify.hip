@@ -7,12 +7,12 @@
 // positions in parallel and then takes the first rejection.  Four launches,
 // each reading what the previous one wrote:
 //
-//   1. verify_stats   grid (rows x 32768-element chunks): one HBM read of
-//                     every target and draft row; per chunk the row max,
+//   1. verify_stats   one wave per 2048-element chunk of every target and
+//                     draft row (one HBM read): the chunk max,
 //                     sum exp((x - m) / T) (fp32 exp2 terms, fp64 sums) and
 //                     the logit at the drafted token, or for greedy rows the
 //                     first argmax / first NaN.
-//   2. verify_decide  grid B: one thread per row merges its chunks, one lane
+//   2. verify_decide  grid B: one wave per row merges its chunks, one lane
 //                     per position runs the accept test with Python's
 //                     min/max semantics; a test whose ratio lies within the
 //                     normalisers' error bound of its uniform is re-decided
@@ -127,89 +127,17 @@ __device__ inline int row_argmax(const float* row, int V, double* red_d, int* re
 }
 
 // ------------------------------------------------------------ 1. stats
-// Chunk statistics of one row for greedy rows: first max and first NaN.
-__device__ inline void stats_greedy(const float* row, int lo, int hi, ChunkStats* out,
-                                    double* red_d, int* red_i) {
-  const int t = threadIdx.x;
-  const bool vec = (((uintptr_t)row) & 15) == 0;
-  const int64_t v0 = vec ? lo / 4 : 0, v1 = vec ? hi / 4 : 0;
-  const f32x4* vp = (const f32x4*)row;
-  float bv = -__builtin_inff();
-  int bi = INT_MAX, ni = INT_MAX;
-  for (int64_t vi = v0 + t; vi < v1; vi += WG) {
-    f32x4 q = __builtin_nontemporal_load(&vp[vi]);
-    float x[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (x[j] > bv) { bv = x[j]; bi = (int)(vi * 4 + j); }
-      if (x[j] != x[j] && ni == INT_MAX) ni = (int)(vi * 4 + j);
-    }
-  }
-  for (int64_t e = (vec ? (v1 * 4 > lo ? v1 * 4 : lo) : lo) + t; e < hi; e += WG) {
-    float x = row[e];
-    if (x > bv) { bv = x; bi = (int)e; }
-    if (x != x && ni == INT_MAX) ni = (int)e;
-  }
-  double dv = bi == INT_MAX ? -__builtin_inf() : (double)bv;
-  block_argmax(dv, bi, red_d, red_i);
-  ni = block_min(ni, red_i, INT_MAX);
-  if (t == 0) { out->bv = (float)dv; out->bi = bi; out->nan_i = ni; out->m = 0; out->s = 0; }
-}
+static_assert(VCHUNK == 64 * 32, "a stats partial is one wave of 8 float4 per lane");
 
-// Chunk statistics of one row for stochastic rows: max of x and
-// sum exp2((x - max) * c), c = log2(e) / T.
-__device__ inline void stats_stoch(const float* row, int lo, int hi, float T, ChunkStats* out,
-                                   double* red_d) {
-  const int t = threadIdx.x;
-  const bool vec = (((uintptr_t)row) & 15) == 0;
-  const int64_t v0 = vec ? lo / 4 : 0, v1 = vec ? hi / 4 : 0;
-  const f32x4* vp = (const f32x4*)row;
-  const float c = (float)(1.4426950408889634 / (double)T);
-  float m = -__builtin_inff();
-  double s = 0.0;
-  constexpr int U = 4;
-  for (int64_t base = v0 + t; base < v1; base += (int64_t)U * WG) {
-    f32x4 q[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-      if (base + u * WG < v1) q[u] = __builtin_nontemporal_load(&vp[base + u * WG]);
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (base + u * WG >= v1) break;
-      float x[4] = {q[u].x, q[u].y, q[u].z, q[u].w};
-      float vm = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-      if (vm > m) {
-        if (s != 0.0) s *= exp2((double)(m - vm) * (double)c);
-        m = vm;
-      }
-      const float mm = fmaxf(m, -3.402823466e38f);
-      float ts = 0.f;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) ts += __builtin_amdgcn_exp2f((x[j] - mm) * c);
-      s += (double)ts;
-    }
-  }
-  for (int64_t e = (vec ? (v1 * 4 > lo ? v1 * 4 : lo) : lo) + t; e < hi; e += WG) {
-    float x = row[e];
-    if (x > m) {
-      if (s != 0.0) s *= exp2((double)(m - x) * (double)c);
-      m = x;
-    }
-    s += (double)__builtin_amdgcn_exp2f((x - fmaxf(m, -3.402823466e38f)) * c);
-  }
-  float M = block_max(m, (float*)red_d, -__builtin_inff());
-  double sc = s != 0.0 ? s * exp2((double)(m - M) * (double)c) : 0.0;
-  double S = block_sum(sc, red_d);
-  if (t == 0) { out->m = M; out->s = S; out->bi = INT_MAX; out->nan_i = INT_MAX; out->bv = 0; }
-}
-
+// One wave per 2048-element chunk of a row: every load in flight at once,
+// wave-level reductions only (no barriers), one ChunkStats per wave.
 __global__ __launch_bounds__(WG) void verify_stats(VerifyArgs A) {
-  __shared__ double red_d[2 * NWAVE + 4];
-  __shared__ int red_i[2 * NWAVE + 4];
   const int g = A.gamma;
   const int nt = A.B * (g + 1);
-  const int r = blockIdx.x / A.nchunk;
-  const int ch = blockIdx.x % A.nchunk;
+  const int per_row = (A.nchunk + NWAVE - 1) / NWAVE;
+  const int r = blockIdx.x / per_row;
+  const int ch = (blockIdx.x % per_row) * NWAVE + wave_id();
+  if (ch >= A.nchunk) return;
   int b, i;
   const float* row;
   bool target;
@@ -218,77 +146,133 @@ __global__ __launch_bounds__(WG) void verify_stats(VerifyArgs A) {
   const float T = A.temperature[b];
   const bool greedy = T == 0.0f;
   if (greedy && !target) return;                     // greedy never reads q rows
+  const int l = lane_id();
   const int lo = ch * VCHUNK, hi = min(A.V, lo + VCHUNK);
-  ChunkStats* out = A.cstats + (size_t)r * A.nchunk + ch;
-  if (greedy) stats_greedy(row, lo, hi, out, red_d, red_i);
-  else stats_stoch(row, lo, hi, T, out, red_d);
-  if (threadIdx.x == 0) {
-    const int tok = i < g ? A.draft_ids[(size_t)b * g + i] : -1;
-    const bool here = tok >= lo && tok < hi;
-    out->has_xt = here ? 1 : 0;
-    out->xt = here ? row[tok] : 0.0f;
+  float x[32];
+  if (hi - lo == VCHUNK && (((uintptr_t)(row + lo)) & 15) == 0) {
+    const f32x4* vp = (const f32x4*)(row + lo);
+    f32x4 q[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) q[j] = __builtin_nontemporal_load(&vp[j * 64 + l]);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      x[4 * j] = q[j].x; x[4 * j + 1] = q[j].y; x[4 * j + 2] = q[j].z; x[4 * j + 3] = q[j].w;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int e = lo + (j * 64 + l) * 4 + c;
+        x[4 * j + c] = e < hi ? row[e] : -__builtin_inff();
+      }
+  }
+  // element index of x[4 j + c]: lo + (j * 64 + l) * 4 + c
+  ChunkStats cs;
+  cs.m = 0.0f; cs.bv = 0.0f; cs.bi = INT_MAX; cs.nan_i = INT_MAX; cs.s = 0.0;
+  if (greedy) {
+    // first maximum: the largest (orderable value, ~index) key; NaN apart
+    uint64_t key = 0;
+    int ni = INT_MAX;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const float v = x[4 * j + c];
+        const int e = lo + (j * 64 + l) * 4 + c;
+        if (v != v) { ni = min(ni, e); continue; }
+        if (e >= hi) continue;
+        const uint64_t k = ((uint64_t)f2key(v) << 32) | (uint32_t)~(uint32_t)e;
+        key = k > key ? k : key;
+      }
+    key = wave_reduce(key, OpMax());
+    ni = wave_reduce(ni, OpMin());
+    if (key != 0) { cs.bv = key2f((uint32_t)(key >> 32)); cs.bi = (int)~(uint32_t)key; }
+    cs.nan_i = ni;
+  } else {
+    float m = -__builtin_inff();
+#pragma unroll
+    for (int k = 0; k < 32; ++k) m = fmaxf(m, x[k]);
+    const float M = wave_reduce(m, OpMax());
+    const float mm = fmaxf(M, -3.402823466e38f);
+    const float c = (float)(1.4426950408889634 / (double)T);
+    double sd = 0.0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {                     // four fp32 terms, then fp64
+      float ts = 0.f;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) ts += __builtin_amdgcn_exp2f((x[4 * j + k] - mm) * c);
+      sd += (double)ts;
+    }
+    cs.m = M;
+    cs.s = wave_reduce(sd, OpAdd());
+  }
+  const int tok = i < g ? A.draft_ids[(size_t)b * g + i] : -1;
+  const bool here = tok >= lo && tok < hi;
+  cs.has_xt = here ? 1 : 0;
+  cs.xt = 0.0f;
+  if (l == 0) {
+    if (here) cs.xt = row[tok];
+    A.cstats[(size_t)r * A.nchunk + ch] = cs;
   }
 }
 
 // ------------------------------------------------------------ 2. decide
-constexpr int MERGE_GROUP = 8;          // chunk statistics loaded at once per row
-
-// Merge the chunk statistics of stochastic row r: max of x, sum
+// Merge the chunk statistics of stochastic row r (one wave): max of x, sum
 // exp((x - max) / T) and the logit at the drafted token.
 __device__ inline void merge_row(const VerifyArgs& A, int r, float T, float& M, double& S,
                                  float& xt) {
   const ChunkStats* cs = A.cstats + (size_t)r * A.nchunk;
   const double c = (double)(float)(1.4426950408889634 / (double)T);
-  M = -__builtin_inff();
-  S = 0.0;
-  xt = 0.0f;
-  bool nan = false;
-  for (int k0 = 0; k0 < A.nchunk; k0 += MERGE_GROUP) {
-    float m[MERGE_GROUP];
-    double s[MERGE_GROUP];
+  const int l = lane_id();
+  constexpr int PL = 8;                               // partials per lane (nchunk <= 512)
+  float m[PL];
+  double s[PL];
+  float xv = 0.0f;
+  int has = 0;
 #pragma unroll
-    for (int j = 0; j < MERGE_GROUP; ++j) {
-      const bool in = k0 + j < A.nchunk;
-      m[j] = in ? cs[k0 + j].m : -__builtin_inff();
-      s[j] = in ? cs[k0 + j].s : 0.0;
-      if (in && cs[k0 + j].has_xt) xt = cs[k0 + j].xt;
-    }
-    float gm = M;
-#pragma unroll
-    for (int j = 0; j < MERGE_GROUP; ++j) gm = fmaxf(gm, m[j]);
-    if (S != 0.0) S *= exp2((double)(M - gm) * c);
-    M = gm;
-#pragma unroll
-    for (int j = 0; j < MERGE_GROUP; ++j) {
-      nan |= s[j] != s[j];
-      if (s[j] != 0.0) S += s[j] * exp2((double)(m[j] - M) * c);
-    }
+  for (int j = 0; j < PL; ++j) {
+    const int k = j * 64 + l;
+    const bool in = k < A.nchunk;
+    m[j] = in ? cs[k].m : -__builtin_inff();
+    s[j] = in ? cs[k].s : 0.0;
+    if (in && cs[k].has_xt) { has = 1; xv = cs[k].xt; }
   }
-  if (nan) S = __builtin_nan("");
+  float lm = -__builtin_inff();
+#pragma unroll
+  for (int j = 0; j < PL; ++j) lm = fmaxf(lm, m[j]);
+  M = wave_reduce(lm, OpMax());
+  double ls = 0.0;
+  int nan = 0;
+#pragma unroll
+  for (int j = 0; j < PL; ++j) {
+    nan |= s[j] != s[j];
+    if (s[j] != 0.0) ls += s[j] * exp2((double)(m[j] - M) * c);
+  }
+  S = wave_reduce(ls, OpAdd());
+  if (wave_reduce(nan, OpMax())) S = __builtin_nan("");
+  const uint64_t hb = __ballot(has);
+  xt = hb ? lane_read(xv, __builtin_ctzll(hb)) : 0.0f;
 }
 
-// First maximum / first NaN of greedy row r from its chunk statistics.
+// First maximum / first NaN of greedy row r from its chunk statistics (one
+// wave).
 __device__ inline int merge_greedy(const VerifyArgs& A, int r) {
   const ChunkStats* cs = A.cstats + (size_t)r * A.nchunk;
-  double bv = -__builtin_inf();
-  int bi = INT_MAX, ni = INT_MAX;
-  for (int k0 = 0; k0 < A.nchunk; k0 += MERGE_GROUP) {
-    float v[MERGE_GROUP];
-    int i[MERGE_GROUP], n[MERGE_GROUP];
-#pragma unroll
-    for (int j = 0; j < MERGE_GROUP; ++j) {
-      const bool in = k0 + j < A.nchunk;
-      v[j] = in ? cs[k0 + j].bv : 0.0f;
-      i[j] = in ? cs[k0 + j].bi : INT_MAX;
-      n[j] = in ? cs[k0 + j].nan_i : INT_MAX;
+  const int l = lane_id();
+  uint64_t key = 0;
+  int ni = INT_MAX;
+  for (int k = l; k < A.nchunk; k += 64) {
+    const ChunkStats c = cs[k];
+    if (c.bi != INT_MAX) {
+      const uint64_t kk = ((uint64_t)f2key(c.bv) << 32) | (uint32_t)~(uint32_t)c.bi;
+      key = kk > key ? kk : key;
     }
-#pragma unroll
-    for (int j = 0; j < MERGE_GROUP; ++j) {
-      if (i[j] != INT_MAX) argmax_merge(bv, bi, (double)v[j], i[j]);
-      ni = min(ni, n[j]);
-    }
+    ni = min(ni, c.nan_i);
   }
-  return ni != INT_MAX ? ni : (bi == INT_MAX ? 0 : bi);
+  key = wave_reduce(key, OpMax());
+  ni = wave_reduce(ni, OpMin());
+  return ni != INT_MAX ? ni : (key == 0 ? 0 : (int)~(uint32_t)key);
 }
 
 __global__ __launch_bounds__(WG) void verify_decide(VerifyArgs A) {
@@ -312,7 +296,10 @@ __global__ __launch_bounds__(WG) void verify_decide(VerifyArgs A) {
   out.rej1 = 0; out.exact = 0; out.Mt = 0.f; out.Mq = 0.f;
   out.St = 0.0; out.Sq = 0.0; out.R = 0.0; out.pad = 0.0;
   if (T == 0.0f) {                                    // speculative.py:150-155
-    for (int i = t; i <= g; i += WG) s_best[i] = merge_greedy(A, b * (g + 1) + i);
+    for (int i = wave_id(); i <= g; i += NWAVE) {
+      const int best = merge_greedy(A, b * (g + 1) + i);
+      if (lane_id() == 0) s_best[i] = best;
+    }
     __syncthreads();
     if (t == 0) {
       int acc = 0;
@@ -338,13 +325,13 @@ __global__ __launch_bounds__(WG) void verify_decide(VerifyArgs A) {
     }
     return;
   }
-  // one thread per row: target rows 0..g-1 at [0, g), draft rows at [g, 2g)
-  for (int j = t; j < 2 * g; j += WG) {
+  // one wave per row: target rows 0..g-1 at [0, g), draft rows at [g, 2g)
+  for (int j = wave_id(); j < 2 * g; j += NWAVE) {
     const int r = j < g ? b * (g + 1) + j : nt + b * g + (j - g);
     float M, xt;
     double S;
     merge_row(A, r, T, M, S, xt);
-    s_M[j] = M; s_S[j] = S; s_x[j] = xt;
+    if (lane_id() == 0) { s_M[j] = M; s_S[j] = S; s_x[j] = xt; }
   }
   __syncthreads();
   const double* ub = A.u + (size_t)b * (g + 1);
@@ -444,6 +431,23 @@ __device__ __forceinline__ void load8(const float* row, int e0, int hi, float (&
 
 static_assert(SUB == 64 * 8, "a normaliser partial is one wave of 8 elements per lane");
 
+// e = exp(fl32(xt / T) - zmt) and f = exp(fl32(xq / T) - zmq) for eight
+// elements (zero past hi); UNIT: T == 1, so fl32(x / T) = x.
+template <bool UNIT>
+__device__ __forceinline__ void pair_terms(const float (&xt)[8], const float (&xq)[8], int e0,
+                                           int hi, double invT, double zmt, double zmq,
+                                           const double* tab, double (&ev)[8],
+                                           double (&fv)[8]) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {                       // branch-free: the exps interleave
+    const bool in = e0 + j < hi;
+    const double zt = UNIT ? (double)xt[j] : div32(xt[j], invT);
+    const double zq = UNIT ? (double)xq[j] : div32(xq[j], invT);
+    ev[j] = in ? exp64_neg(zt - zmt, tab) : 0.0;
+    fv[j] = in ? exp64_neg(zq - zmq, tab) : 0.0;
+  }
+}
+
 // One wave per 512-element sub-chunk of the rejected row pair.
 __global__ __launch_bounds__(WG) void verify_norm(VerifyArgs A) {
   __shared__ double tab[64];
@@ -468,12 +472,8 @@ __global__ __launch_bounds__(WG) void verify_norm(VerifyArgs A) {
   load8(tr, e0, A.V, xt);
   load8(dr, e0, A.V, xq);
   double ev[8], fv[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {                       // branch-free: the exps interleave
-    const bool in = e0 + j < A.V;
-    ev[j] = in ? exp64(div32(xt[j], invT) - zmt, tab) : 0.0;
-    fv[j] = in ? exp64(div32(xq[j], invT) - zmq, tab) : 0.0;
-  }
+  if (T == 1.0f) pair_terms<true>(xt, xq, e0, A.V, invT, zmt, zmq, tab, ev, fv);
+  else pair_terms<false>(xt, xq, e0, A.V, invT, zmt, zmq, tab, ev, fv);
   double se = 0.0, sf = 0.0, dp = 0.0, fp = 0.0;
   unsigned amb = 0;
 #pragma unroll
@@ -586,7 +586,8 @@ __global__ __launch_bounds__(WG) void verify_draw(VerifyArgs A) {
     const int e = sidx * SUB + t;
     double d = 0.0;
     if (t < SUB && e < A.V)
-      d = exp64(div32(tr[e], C.invT) - C.zmt, tab) - lam * exp64(div32(dr[e], C.invT) - C.zmq, tab);
+      d = exp64_neg(div32(tr[e], C.invT) - C.zmt, tab) -
+          lam * exp64_neg(div32(dr[e], C.invT) - C.zmq, tab);
     d = block_sum(d > 0.0 ? d : 0.0, red_d);
     if (t == 0) tsum[sidx] = d;
     __syncthreads();
@@ -627,8 +628,8 @@ __global__ __launch_bounds__(WG) void verify_draw(VerifyArgs A) {
       const int e = found * SUB + t;
       double w = 0.0;
       if (t < SUB && e < A.V) {
-        const double d = exp64(div32(tr[e], C.invT) - C.zmt, tab) -
-                         lam * exp64(div32(dr[e], C.invT) - C.zmq, tab);
+        const double d = exp64_neg(div32(tr[e], C.invT) - C.zmt, tab) -
+                         lam * exp64_neg(div32(dr[e], C.invT) - C.zmq, tab);
         w = d > 0.0 ? d : 0.0;
       }
       if (t < SUB) tsum[t] = w;
@@ -665,7 +666,8 @@ __global__ __launch_bounds__(WG) void verify_draw(VerifyArgs A) {
 int launch_verify(const VerifyArgs& A, bool any_stochastic, hipStream_t s) {
   const int nt = A.B * (A.gamma + 1);
   const int nrows = nt + (any_stochastic ? A.B * A.gamma : 0);
-  timed_launch(CX_KERNEL_VERIFY_STATS, verify_stats, dim3(nrows * A.nchunk), dim3(WG), 0, s, A);
+  const int per_row = (A.nchunk + NWAVE - 1) / NWAVE;
+  timed_launch(CX_KERNEL_VERIFY_STATS, verify_stats, dim3(nrows * per_row), dim3(WG), 0, s, A);
   timed_launch(CX_KERNEL_VERIFY_REST, verify_decide, dim3(A.B), dim3(WG), 0, s, A);
   if (any_stochastic) {
     const int per_b = (A.nsub + NWAVE - 1) / NWAVE;
