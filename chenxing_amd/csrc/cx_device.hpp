@@ -17,6 +17,20 @@ constexpr int NWAVE = WG / 64;
 // become flat instructions (which also wait on outstanding global loads);
 // address space 3 keeps them ds_* operations.
 #define CX_LDS __attribute__((address_space(3)))
+// Read-only kernel inputs read through the constant address space: uniform
+// reads become scalar loads (SMEM), which complete independently of the
+// vector loads in flight.
+#define CX_CONST __attribute__((address_space(4)))
+template <typename T>
+__device__ __forceinline__ T const_load(const T* p) {
+  static_assert(sizeof(T) % 4 == 0, "whole dwords");
+  T v;
+  const CX_CONST uint32_t* s = (const CX_CONST uint32_t*)p;
+  uint32_t* d = (uint32_t*)&v;
+#pragma unroll
+  for (int i = 0; i < (int)(sizeof(T) / 4); ++i) d[i] = s[i];
+  return v;
+}
 template <typename T>
 __device__ __forceinline__ CX_LDS T* to_lds(T* p) { return (CX_LDS T*)p; }
 template <typename T>

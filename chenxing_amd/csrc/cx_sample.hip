@@ -40,6 +40,15 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 #define CX_RELAXED_WG __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP
 
+// The row's 64-byte parameter block in one scalar load (uniform, SGPRs):
+// it does not wait behind the vector loads in flight.
+__device__ __forceinline__ cx_row_params sload_params(const cx_row_params* p) {
+  typedef uint32_t u32x16 __attribute__((ext_vector_type(16)));
+  u32x16 v;
+  asm volatile("s_load_dwordx16 %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p));
+  return __builtin_bit_cast(cx_row_params, v);
+}
+
 // ------------------------------------------------------------ penalties
 // Penalty index of a slice [lo, hi): a bitmap of the window's ids (the
 // stream's test) and an open-addressing hash of the distinct ids, one word
@@ -56,6 +65,8 @@ struct PenIndex {
 constexpr uint32_t HW_EMPTY = 0xFFFFFFFFu;
 constexpr int NSLOT = 4;                        // published lane keys per wave
 constexpr int HPT = (WIN_MAX + WG - 1) / WG;   // window entries per thread
+constexpr int NS_MAX = 8192;                    // most index slots (2 x WIN_MAX, power of two)
+static_assert(NS_MAX >= 2 * WIN_MAX && NS_MAX % (64 * NWAVE) == 0, "index slot groups");
 
 __device__ __forceinline__ bool pen_bit(const PenIndex& X, int r) {
   return (X.bitmap[r >> 5] >> (r & 31)) & 1u;
@@ -126,22 +137,23 @@ template <> struct Elem<true> {
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const void* p, int bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, bytes, 0x00020000);
 }
-// 16-byte nontemporal load at byte offset voff + soff (soff wave-uniform).
+// 16-byte nontemporal load at byte offset voff (range-checked: past the
+// descriptor's end it returns 0 and touches no memory).
 template <bool BF16>
-__device__ __forceinline__ typename Elem<BF16>::V bload(__amdgpu_buffer_rsrc_t rs, int voff,
-                                                       int soff) {
+__device__ __forceinline__ typename Elem<BF16>::V bload(__amdgpu_buffer_rsrc_t rs, int voff) {
   return __builtin_bit_cast(typename Elem<BF16>::V,
-                            __builtin_amdgcn_raw_buffer_load_b128(rs, voff, soff, 2));
+                            __builtin_amdgcn_raw_buffer_load_b128(rs, voff, 0, 2));
 }
 // The U vectors of this lane in chunk ch: vectors ch * 64U + u * 64 + lane.
+// Issued unconditionally, also for chunk ids past the slice (their loads
+// return zeros that are never used): the compiler then knows exactly how
+// many loads are in flight and waits only for the chunk being consumed.
 template <bool BF16>
 __device__ __forceinline__ void load_chunk(__amdgpu_buffer_rsrc_t rs, int ch,
                                            typename Elem<BF16>::V (&q)[Elem<BF16>::U]) {
   constexpr int U = Elem<BF16>::U;
 #pragma unroll
-  for (int u = 0; u < U; ++u)
-    q[u] = bload<BF16>(rs, lane_id() * 16,
-                       __builtin_amdgcn_readfirstlane((ch * 64 * U + u * 64) * 16));
+  for (int u = 0; u < U; ++u) q[u] = bload<BF16>(rs, ((ch * 64 * U + u * 64) + lane_id()) * 16);
 }
 // Next chunk for this wave from the workgroup's counter.
 __device__ __forceinline__ int next_chunk(CX_LDS int* counter) {
@@ -425,9 +437,10 @@ __device__ __forceinline__ void append_chunk(WaveBuf& wb,
 
 // Stream the vectors of a stochastic slice.  Vector i covers elements
 // lo + i*NE .. lo + i*NE + NE-1, i < nv.  q and qn hold this wave's first
-// two chunks (wave_id() and wave_id() + NWAVE), loaded by the caller; every
-// iteration processes q and then asks for the chunk after qn, so two chunks
-// stay in flight.
+// two chunks (wave_id() and wave_id() + NWAVE), loaded by the caller.  The
+// loop alternates between the two buffers (no register copies, which would
+// wait for the chunk still in flight): it consumes one and refills it with
+// the chunk after the other, so two chunks stay in flight.
 template <bool BF16>
 __device__ __forceinline__ void stream_stoch(__amdgpu_buffer_rsrc_t rs,
                                              typename Elem<BF16>::V (&q)[Elem<BF16>::U],
@@ -437,6 +450,7 @@ __device__ __forceinline__ void stream_stoch(__amdgpu_buffer_rsrc_t rs,
                                              CX_LDS uint32_t* slots, CX_LDS uint32_t* w_pub,
                                              SState& st, WaveBuf& wb, uint32_t& ck) {
   using E = Elem<BF16>;
+  using V = typename E::V;
   constexpr int NE = E::NE;
   constexpr int U = E::U;
   constexpr int CH = 64 * U;
@@ -444,17 +458,18 @@ __device__ __forceinline__ void stream_stoch(__amdgpu_buffer_rsrc_t rs,
   const bool share = true;
   const int nch = (nv + CH - 1) / CH;
   const int nfull = nv / CH;
-  // chunk ids are wave-uniform (SGPRs): readfirstlane keeps the buffer
-  // offsets scalar
+  // chunk ids are wave-uniform (SGPRs)
   int ch = __builtin_amdgcn_readfirstlane(wave_id());
   int cn = ch + NWAVE;
   bool fresh = false;              // appended since the last publication
-  for (int it = 0; ch < nch; ++it) {
+  int it = 0;
+  // consume chunk ch from buffer b, refill b with the chunk after cn
+  auto step = [&](V (&b)[U]) {
     raise_tau(wb, lds_load(wb.shared));
     const int vb = ch * CH + lane_id();
     float x[U][NE];
 #pragma unroll
-    for (int u = 0; u < U; ++u) E::unpack(q[u], x[u]);
+    for (int u = 0; u < U; ++u) E::unpack(b[u], x[u]);
     if (ch >= nfull) {                 // the last, partial chunk
 #pragma unroll
       for (int u = 0; u < U; ++u)
@@ -481,13 +496,16 @@ __device__ __forceinline__ void stream_stoch(__amdgpu_buffer_rsrc_t rs,
       raise_tau(wb, lds_load(wb.shared));
       fresh = false;
     }
-    // next: q <- qn, and the chunk after it into qn
     const int cnn = cn < nch ? __builtin_amdgcn_readfirstlane(next_chunk(chunk_ctr)) : nch;
-#pragma unroll
-    for (int u = 0; u < U; ++u) q[u] = qn[u];
-    if (cnn < nch) load_chunk<BF16>(rs, cnn, qn);
+    load_chunk<BF16>(rs, cnn, b);      // past the slice: zeros, never consumed
     ch = cn;
     cn = cnn;
+    ++it;
+  };
+  while (ch < nch) {
+    step(q);
+    if (ch >= nch) break;
+    step(qn);
   }
 }
 
@@ -549,27 +567,32 @@ __device__ __forceinline__ void stream_greedy(const char* rowp, __amdgpu_buffer_
                                               const PenIndex& X, CX_LDS int* chunk_ctr,
                                               GreedyState& gs) {
   using E = Elem<BF16>;
+  using V = typename E::V;
   constexpr int NE = E::NE;
   constexpr int U = E::U;
   constexpr int CH = 64 * U;
   const int nch = (nv + CH - 1) / CH;
   int ch = __builtin_amdgcn_readfirstlane(wave_id());
   int cn = ch + NWAVE;
-  while (ch < nch) {
+  // the two buffers alternate, as in stream_stoch
+  auto step = [&](V (&b)[U]) {
     const int vb = ch * CH + lane_id();
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       float x[NE];
-      E::unpack(q[u], x);
+      E::unpack(b[u], x);
       const int vi = vb + u * 64;
       greedy_vec<NE>(x, vi * NE + lo, vi < nv, lo, pen_on, X, gs);
     }
     const int cnn = cn < nch ? __builtin_amdgcn_readfirstlane(next_chunk(chunk_ctr)) : nch;
-#pragma unroll
-    for (int u = 0; u < U; ++u) q[u] = qn[u];
-    if (cnn < nch) load_chunk<BF16>(rs, cnn, qn);
+    load_chunk<BF16>(rs, cnn, b);
     ch = cn;
     cn = cnn;
+  };
+  while (ch < nch) {
+    step(q);
+    if (ch >= nch) break;
+    step(qn);
   }
   for (int e = s0 + threadIdx.x; e < hi; e += WG) {
     float x1[1] = {E::scalar(rowp, e)};
@@ -726,6 +749,70 @@ struct PenRec {
   int fl, pad;
 };
 
+// Wave w owns the 64-slot groups w, w + NWAVE, ... of the penalty index
+// once the index is built: after its stream it loads their raw logits,
+// computes their penalised values, the region pre-test copies and its share
+// of the penalty corrections to the sum.
+constexpr int GPW = NS_MAX / (64 * NWAVE);      // slot groups per wave at most
+
+// Issue the loads of the wave's owned ids' raw logits (to be consumed by
+// pen_correct after other work).
+template <bool BF16>
+__device__ __forceinline__ void pen_fetch(const PenIndex& X, const char* rowp,
+                                          float (&raw)[GPW]) {
+  using E = Elem<BF16>;
+#pragma unroll
+  for (int g = 0; g < GPW; ++g) {
+    const int s = (g * NWAVE + wave_id()) * 64 + lane_id();
+    const uint32_t hw = s < X.ns ? X.hword[s] : HW_EMPTY;
+    raw[g] = hw != HW_EMPTY ? E::scalar(rowp, (int)(hw >> 12)) : 0.0f;
+  }
+}
+
+// The wave's penalty corrections: hval = raw logit, hpen = fp32(penalised
+// value), and against Rc = ceil(max * c) the sums of the raw terms (pr) and
+// of penalised minus raw terms (corr), fp32 terms each <= 1 and within TOL_T
+// of the exact ones.
+__device__ __forceinline__ void pen_correct(const PenIndex& X, const float (&raw)[GPW],
+                                            const cx_row_params& P, double kc, PenRec* rec) {
+  double pm = -__builtin_inf();
+  double xp[GPW];
+#pragma unroll
+  for (int g = 0; g < GPW; ++g) {
+    const int s = (g * NWAVE + wave_id()) * 64 + lane_id();
+    const uint32_t hw = s < X.ns ? X.hword[s] : HW_EMPTY;
+    xp[g] = 0.0;
+    if (hw == HW_EMPTY) continue;
+    xp[g] = penalise(raw[g], (int)(hw & 0xFFFu), P);
+    X.hval[s] = raw[g];
+    X.hpen[s] = (float)xp[g];
+    pm = (double)raw[g] > pm ? (double)raw[g] : pm;
+    pm = xp[g] > pm ? xp[g] : pm;
+  }
+  pm = wave_reduce(pm, OpMax());
+  // NaN / +-inf windows leave Rc at 0 (their rows go to the exact kernel)
+  const double Rc = (pm > -__builtin_inf() && pm < __builtin_inf()) ? ceil(pm * kc) : 0.0;
+  double corr = 0.0, pr = 0.0, pmx = -__builtin_inf();
+  int fl = 0;
+#pragma unroll
+  for (int g = 0; g < GPW; ++g) {
+    const int s = (g * NWAVE + wave_id()) * 64 + lane_id();
+    const uint32_t hw = s < X.ns ? X.hword[s] : HW_EMPTY;
+    if (hw == HW_EMPTY) continue;
+    const double tr = (double)__builtin_amdgcn_exp2f((float)((double)raw[g] * kc - Rc));
+    const double tp = (double)__builtin_amdgcn_exp2f((float)(xp[g] * kc - Rc));
+    pr += tr;
+    corr += tp - tr;
+    if (xp[g] != xp[g]) fl = 1;
+    else pmx = xp[g] > pmx ? xp[g] : pmx;
+  }
+  corr = wave_reduce(corr, OpAdd());
+  pr = wave_reduce(pr, OpAdd());
+  pmx = wave_reduce(pmx, OpMax());
+  fl = wave_reduce(fl, OpOr());
+  if (lane_id() == 0) { rec->corr = corr; rec->pr = pr; rec->pmx = pmx; rec->Rc = Rc; rec->fl = fl; }
+}
+
 // ------------------------------------------------------------ the kernel
 template <bool BF16>
 __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
@@ -756,8 +843,9 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   // the row's parameters live in LDS after the first barrier (P), not in
   // registers across the stream; P0 serves the prologue
   __shared__ cx_row_params sP;
-  const cx_row_params P0 = A.prm[row];
-  const double u_row = A.u[row];
+  const cx_row_params P0 = sload_params(A.prm + row);
+  if (t == 0) sP = P0;
+  const double u_row = const_load(A.u + row);
   const bool greedy = P0.temperature == 0.0;
   const int lo = split * A.split_len;
   const int hi = min(A.V, lo + A.split_len);
@@ -766,7 +854,7 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
 
   int wlen = 0, wstart = 0;
   if (A.ldh > 0) {
-    int len = max(0, min(A.hist_len[row], (int)A.ldh));
+    int len = max(0, min(const_load(A.hist_len + row), (int)A.ldh));
     wstart = P0.n_keep > 0 ? max(0, len - max(64, P0.n_keep)) : 0;
     wlen = len - wstart;
   }
@@ -787,19 +875,22 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   // the window ids first, then this wave's first two chunks (wave_id and
   // wave_id + NWAVE; the LDS counter hands out the rest from 2 * NWAVE on):
   // all in flight while the index tables are cleared
-  int32_t hid[HPT];
+  // (all unconditional buffer loads, so waiting for the ids does not wait
+  // for the chunks)
+  const __amdgpu_buffer_rsrc_t hrs =
+      row_rsrc(pen_on ? (const void*)(A.hist + (size_t)row * A.ldh + wstart) : nullptr,
+               pen_on ? wlen * 4 : 0);
+  int32_t hid[HPT];                  // raw; entries at or past wlen are ignored
 #pragma unroll
-  for (int k = 0; k < HPT; ++k) {
-    const int i = t + k * WG;
-    hid[k] = (pen_on && i < wlen) ? A.hist[(size_t)row * A.ldh + wstart + i] : -1;
-  }
+  for (int k = 0; k < HPT; ++k)
+    hid[k] = (int)__builtin_amdgcn_raw_buffer_load_b32(hrs, (t + k * WG) * 4, 0, 0);
   const int nv = A.vec_ok ? (hi - lo) / NE : 0;       // whole vectors of the slice
   const int s0 = lo + nv * NE;                         // first scalar element
   const __amdgpu_buffer_rsrc_t rs = row_rsrc(rowp + (size_t)lo * (BF16 ? 2 : 4), nv * 16);
   const int ch0 = __builtin_amdgcn_readfirstlane(wave_id());
   typename E::V q[U], qn[U];
-  if (ch0 * CH < nv) load_chunk<BF16>(rs, ch0, q);
-  if ((ch0 + NWAVE) * CH < nv) load_chunk<BF16>(rs, ch0 + NWAVE, qn);
+  load_chunk<BF16>(rs, ch0, q);
+  load_chunk<BF16>(rs, ch0 + NWAVE, qn);
 
   PenIndex X;
   X.bitmap = to_lds((uint32_t*)(dyn + A.off_bitmap));
@@ -809,7 +900,7 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   X.nbw = (hi - lo + 31) >> 5;
   X.ns = pen_on ? A.ns : 0;
   X.ns_log2 = A.ns_log2;
-  if (t == 0) { s_shared = 1u; s_chunk = 2 * NWAVE; s_cnt = 0; s_done = 0; sP = P0; }
+  if (t == 0) { s_shared = 1u; s_chunk = 2 * NWAVE; s_cnt = 0; s_done = 0; }
   if (t < NWAVE) { w_pub[t] = 0u; w_cnt[t] = 0; }
   if (t < 4 * NWAVE) slots[t] = 0u;
   if (pen_on) {
@@ -818,27 +909,18 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   }
   __syncthreads();
   const cx_row_params& P = sP;
-  // index the window ids of this slice; the thread that inserts a distinct
-  // id owns it and fetches its raw logit (stored to the index before the
-  // stream starts)
-  int hslot[HPT];
-  float gval[HPT];
-#pragma unroll
-  for (int k = 0; k < HPT; ++k)
-    gval[k] = (!greedy && hid[k] >= lo && hid[k] < hi) ? E::scalar(rowp, hid[k]) : 0.0f;
+  // index the window ids of this slice: a bitmap bit and a hash word
+  // (id << 12 | count) per distinct id
 #pragma unroll
   for (int k = 0; k < HPT; ++k) {
     const int id = hid[k];
-    hslot[k] = -1;
-    if (id >= lo && id < hi) {
+    if (pen_on && t + k * WG < wlen && id >= lo && id < hi) {
       __hip_atomic_fetch_or(X.bitmap + ((id - lo) >> 5), 1u << ((id - lo) & 31), CX_RELAXED_WG);
       bool created;
-      const int h = pen_insert(X, id, created);
-      if (created) hslot[k] = h;
+      pen_insert(X, id, created);
     }
   }
   __syncthreads();
-
   // ---------------------------------------------------------------- greedy
   if (greedy) {
     GreedyState gs{-__builtin_inff(), INT_MAX, INT_MAX};
@@ -912,51 +994,6 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
     const uint32_t th = kth_of_lanes(ck, pub_r);
     if (lane_id() == 0) lpub[wave_id()] = th;
   }
-  // the window ids this wave's threads own: raw logits (and penalised
-  // values, rounded to fp32 for the region test) into the index, the
-  // penalty corrections into the wave's record
-  {
-    double xpk[HPT];
-    double pm = -__builtin_inf();
-#pragma unroll
-    for (int k = 0; k < HPT; ++k) {
-      xpk[k] = 0.0;
-      if (hslot[k] < 0) continue;
-      xpk[k] = penalise(gval[k], (int)(X.hword[hslot[k]] & 0xFFFu), P);
-      X.hval[hslot[k]] = gval[k];
-      X.hpen[hslot[k]] = (float)xpk[k];
-      pm = (double)gval[k] > pm ? (double)gval[k] : pm;
-      pm = xpk[k] > pm ? xpk[k] : pm;
-    }
-    pm = wave_reduce(pm, OpMax());
-    // NaN / +-inf windows leave Rc at 0 (their rows go to the exact kernel)
-    const double Rc = (pm > -__builtin_inf() && pm < __builtin_inf()) ? ceil(pm * kc) : 0.0;
-    double corr = 0.0, pr = 0.0, pmx = -__builtin_inf();
-    int fl = 0;
-#pragma unroll
-    for (int k = 0; k < HPT; ++k) {
-      if (hslot[k] < 0) continue;
-      const double xp = xpk[k];
-      // fp32 terms (each <= 1) are within TOL_T of the exact ones
-      const double tr = (double)__builtin_amdgcn_exp2f((float)((double)gval[k] * kc - Rc));
-      const double tp = (double)__builtin_amdgcn_exp2f((float)(xp * kc - Rc));
-      pr += tr;
-      corr += tp - tr;
-      if (xp != xp) fl = 1;
-      else pmx = xp > pmx ? xp : pmx;
-    }
-    corr = wave_reduce(corr, OpAdd());
-    pr = wave_reduce(pr, OpAdd());
-    pmx = wave_reduce(pmx, OpMax());
-    fl = wave_reduce(fl, OpOr());
-    if (lane_id() == 0) {
-      s_pen[wave_id()].corr = corr;
-      s_pen[wave_id()].pr = pr;
-      s_pen[wave_id()].pmx = pmx;
-      s_pen[wave_id()].Rc = Rc;
-      s_pen[wave_id()].fl = fl;
-    }
-  }
   __syncthreads();
   if (krow <= 64) raise_tau(wb, kth_of_lanes(lds_load(lslots + lane_id()), krow));
   else if (pub_r > 0) raise_tau(wb, pub_min(lpub));
@@ -975,7 +1012,10 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   }
 
   // ---- per wave, after its stream: its region entries into the shared
-  // list, its sums and state for the combination
+  // list (while its owned ids' raw logits are on the way), its penalty
+  // corrections, its sums and state for the combination
+  float raw[GPW];
+  if (pen_on) pen_fetch<BF16>(X, rowp, raw);
   raise_tau(wb, lds_load(wb.shared));
   {
     const int n = wb.n;
@@ -987,13 +1027,17 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
       }
     }
   }
+  if (pen_on) pen_correct(X, raw, P, kc, &s_pen[wave_id()]);
+  else if (lane_id() == 0) {
+    s_pen[wave_id()].corr = 0.0; s_pen[wave_id()].pr = 0.0; s_pen[wave_id()].pmx = -__builtin_inf();
+    s_pen[wave_id()].Rc = 0.0; s_pen[wave_id()].fl = 0;
+  }
   {
     // this wave's share of the window ids: penalised values at or above its
     // threshold (fp32 pre-test, exact value for the survivors)
-    const int per = X.ns / NWAVE;
     const float thr_f = wb.tauf;
     const double thr_w = wb.tau <= 1u ? -__builtin_inf() : (double)wb.tauf;
-    for (int s = wave_id() * per + lane_id(); s < (wave_id() + 1) * per; s += 64) {
+    for (int s = wave_id() * 64 + lane_id(); s < X.ns; s += NWAVE * 64) {
       const uint32_t hw = X.hword[s];
       if (hw == HW_EMPTY) continue;
       // rounding is monotone: xp >= thr_f (a float) implies fp32(xp) >= thr_f
