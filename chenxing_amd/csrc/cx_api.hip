@@ -120,8 +120,8 @@ static int sample_impl(const void* logits, int dtype, int64_t ld, int32_t B, int
   A.vec_ok = (((uintptr_t)logits) % 16 == 0) && ((ld * esz) % 16 == 0);
   slow_layout(A, V, ldh);
   // fused kernel: penalty index (bitmap of the slice's window ids, hash of
-  // (id << 12 | count) words and the ids' raw logits) and the per-wave
-  // candidate buffers
+  // (id << 12 | count) words, the ids' raw logits and the dense list of
+  // occupied slots) and the per-wave candidate buffers
   const long nbw = ldh > 0 ? (A.split_len + 31) / 32 : 0;
   const long nslot = ldh > 0 ? A.ns : 0;
   size_t off = 0;
@@ -131,7 +131,7 @@ static int sample_impl(const void* logits, int dtype, int64_t ld, int32_t B, int
   off += (size_t)nslot * 4;
   A.off_hval = (int)off;
   off += (size_t)nslot * 4;
-  A.off_hpen = (int)off;
+  A.off_dense = (int)off;
   off = align_up(off + (size_t)nslot * 4, 16);
   A.off_wkey = (int)off;
   off += (size_t)16 * CAPW * 4;

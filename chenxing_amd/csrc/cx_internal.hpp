@@ -65,7 +65,7 @@ struct SampleArgs {
   int32_t nsplit, split_len;
   int32_t ns, ns_log2;    // penalty hash slots (power of two, >= 2 x window) and log2
   int32_t vec_ok;         // rows are 16-byte aligned
-  int32_t off_bitmap, off_hword, off_hval, off_hpen, off_wkey, off_widx, off_gather;
+  int32_t off_bitmap, off_hword, off_hval, off_dense, off_wkey, off_widx, off_gather;
   int32_t lds_bytes;      // fused kernel dynamic LDS
   int32_t fin_lds_bytes;  // finish kernel dynamic LDS (several slices per row)
   int32_t bf16;           // logits are bf16 bit patterns

@@ -40,33 +40,54 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 #define CX_RELAXED_WG __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP
 
-// The row's 64-byte parameter block in one scalar load (uniform, SGPRs):
-// it does not wait behind the vector loads in flight.
-__device__ __forceinline__ cx_row_params sload_params(const cx_row_params* p) {
+// The row's scalars -- its 64-byte parameter block, its uniform and its
+// history length -- in three scalar loads under one wait (uniform, SGPRs):
+// they do not wait behind the vector loads in flight.
+struct RowScalars {
+  cx_row_params p;
+  double u;
+  int hlen;
+};
+__device__ __forceinline__ RowScalars sload_row(const cx_row_params* p, const double* u,
+                                                const int32_t* hl) {
   typedef uint32_t u32x16 __attribute__((ext_vector_type(16)));
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
   u32x16 v;
-  asm volatile("s_load_dwordx16 %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p));
-  return __builtin_bit_cast(cx_row_params, v);
+  u32x2 uu;
+  uint32_t h;
+  asm volatile(
+      "s_load_dwordx16 %0, %3, 0x0\n\t"
+      "s_load_dwordx2 %1, %4, 0x0\n\t"
+      "s_load_dword %2, %5, 0x0\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&s"(v), "=&s"(uu), "=&s"(h)
+      : "s"(p), "s"(u), "s"(hl));
+  RowScalars r;
+  r.p = __builtin_bit_cast(cx_row_params, v);
+  r.u = __builtin_bit_cast(double, uu);
+  r.hlen = (int)h;
+  return r;
 }
 
 // ------------------------------------------------------------ penalties
 // Penalty index of a slice [lo, hi): a bitmap of the window's ids (the
-// stream's test) and an open-addressing hash of the distinct ids, one word
-// (id << 12 | count in the window) and the id's raw logit per slot.  Ids are
-// below 2^20 and counts below 2^12, so no word equals HW_EMPTY.
+// stream's test), an open-addressing hash of the distinct ids, one word
+// (id << 12 | count in the window) and the id's raw logit per slot, and the
+// dense list of the occupied slots in insertion order.  Ids are below 2^20
+// and counts below 2^12, so no word equals HW_EMPTY.
 struct PenIndex {
   CX_LDS uint32_t* bitmap;
   CX_LDS uint32_t* hword;
   CX_LDS float* hval;
-  CX_LDS float* hpen;     // penalised value rounded to fp32 (region pre-test)
+  CX_LDS int32_t* dense;
   int nbw;
   int ns, ns_log2;
 };
 constexpr uint32_t HW_EMPTY = 0xFFFFFFFFu;
 constexpr int NSLOT = 4;                        // published lane keys per wave
-constexpr int HPT = (WIN_MAX + WG - 1) / WG;   // window entries per thread
-constexpr int NS_MAX = 8192;                    // most index slots (2 x WIN_MAX, power of two)
-static_assert(NS_MAX >= 2 * WIN_MAX && NS_MAX % (64 * NWAVE) == 0, "index slot groups");
+constexpr int HPT = (WIN_MAX + WG - 1) / WG;   // history entries per thread loaded up front
+constexpr int GD = 1;                           // distinct ids per thread whose raw logits
+                                                // are fetched before the stream
 
 __device__ __forceinline__ bool pen_bit(const PenIndex& X, int r) {
   return (X.bitmap[r >> 5] >> (r & 31)) & 1u;
@@ -600,99 +621,81 @@ __device__ __forceinline__ void stream_greedy(const char* rowp, __amdgpu_buffer_
   }
 }
 
-// ------------------------------------------------------------ one-wave finish
-struct LeanLds {          // one wave's work area (72 slots: unrolled reads overrun)
-  uint64_t k[72];         // kept keys, list order
-  int32_t i[72];
-  uint64_t sk[72];        // rank order
-  int32_t si[72];
-  double q[72];
+// ------------------------------------------------------------ top-k finish
+// Finish of a top-k row (k <= 64) from its region list (nlist <= LEAN_CAP
+// entries with distinct ids, holding every value at or above the k-th
+// largest): the list is ranked by value and by id in parallel, then one
+// wave cuts top-k (ties kept), top-p and min-p on the rank-ordered top
+// entries and draws in token-id order.
+struct LeanLds {
+  int32_t rv[LEAN_CAP];   // value rank of list entry e (descending, ties by ascending id)
+  int32_t ri[LEAN_CAP];   // id rank of list entry e (ascending)
+  uint64_t sk[68];        // keys of value ranks 0..64
+  int32_t si[68];         // their ids
+  int32_t sr[68];         // their id ranks
+  double oq[LEAN_CAP];    // normalised kept mass at id rank r (0 where not kept)
+  int32_t oid[LEAN_CAP];  // id at id rank r
 };
 
-// Wave 0 decides a top-k row (k <= 64) from the region list: the entries at
-// or above thr64 (at most 64, else the cut is raised to the k-th largest)
-// are ranked (value descending, id ascending) by counting, cut by top-k
-// (ties kept), top-p and min-p, and one is drawn in token-id order.
-// Returns false when the row needs the exact path (near a top-p boundary,
-// fewer than k records above a proper threshold, or more than 64 records
-// tied into the top-k).
-__device__ inline bool lean_decide(const SampleArgs& A, int row, const cx_row_params& P,
-                                   const CX_LDS uint64_t* gk, const CX_LDS int32_t* gi, int nlist,
-                                   uint64_t thr64, double kc, double Rb, double S, double tol,
-                                   CX_LDS LeanLds* L, double u, int& tok) {
+// Waves 1 .. NWAVE-1: each counts, for one group of 64 list entries, the
+// entries of one stripe of the list that precede them by value and by id.
+// The counts are integers, so the order of the LDS additions does not
+// matter.  rv and ri start at zero.
+__device__ __forceinline__ void lean_ranks(const CX_LDS uint64_t* gk, const CX_LDS int32_t* gi,
+                                           int nlist, CX_LDS LeanLds* L) {
+  const int ng = (nlist + 63) >> 6;
+  const int per = (NWAVE - 1) / ng;
+  const int w = wave_id() - 1;
+  const int eg = w % ng, sp = w / ng;
+  if (sp >= per) return;
+  const int e = eg * 64 + lane_id();
+  const int j0 = sp * nlist / per, j1 = (sp + 1) * nlist / per;
+  const uint64_t ke = e < nlist ? gk[e] : 0ull;
+  const int32_t ie = e < nlist ? gi[e] : INT_MAX;
+  int cv = 0, ci = 0;
+#pragma unroll 4
+  for (int j = j0; j < j1; ++j) {
+    const uint64_t kj = gk[j];
+    const int32_t ij = gi[j];
+    cv += (kj > ke || (kj == ke && ij < ie)) ? 1 : 0;
+    ci += ij < ie ? 1 : 0;
+  }
+  if (e < nlist) {
+    __hip_atomic_fetch_add(&L->rv[e], cv, CX_RELAXED_WG);
+    __hip_atomic_fetch_add(&L->ri[e], ci, CX_RELAXED_WG);
+  }
+}
+
+// One wave decides the row from the ranks; Rb and S give probabilities
+// exp2(x c - Rb) / S within tol (relative) of the exact ones.  Returns false
+// when the row needs the exact path (near a top-p boundary, or more than
+// 64 entries tied into the top-k).
+__device__ inline bool lean_decide(const cx_row_params& P, const CX_LDS uint64_t* gk,
+                                   const CX_LDS int32_t* gi, int nlist, double kc, double Rb,
+                                   double S, double tol, CX_LDS LeanLds* L, double u, int& tok) {
   const int l = lane_id();
-  constexpr int PER = LEAN_CAP / 64;
-  uint64_t k[PER];
-  int32_t id[PER];
-  int E = 0;
-#pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    const int e = l + 64 * j;
-    k[j] = e < nlist ? gk[e] : 0ull;
-    id[j] = e < nlist ? gi[e] : INT_MAX;
-    if (k[j] < thr64) k[j] = 0ull;
-    E += __popcll(ballot(k[j] != 0ull));
+  // the top 65 entries in value order, and every id at its id rank
+  for (int e = l; e < nlist; e += 64) {
+    const int r = L->rv[e], q = L->ri[e];
+    const int32_t id = gi[e];
+    if (r < 65) { L->sk[r] = gk[e]; L->si[r] = id; L->sr[r] = q; }
+    L->oid[q] = id;
+    L->oq[q] = 0.0;
   }
-  if (E < P.top_k && thr64 > 1ull) return false;
-  uint64_t cut = 1ull;
-  if (E > 64) {
-    // raise the cut to the k-th largest kept key, two bits per step
-    uint64_t prefix = 0ull;
-    for (int sh = 62; sh >= 0; sh -= 2) {
-      const uint64_t b1 = prefix | (1ull << sh), b2 = prefix | (2ull << sh),
-                     b3 = prefix | (3ull << sh);
-      int c1 = 0, c2 = 0, c3 = 0;
-#pragma unroll
-      for (int j = 0; j < PER; ++j) {
-        c3 += __popcll(ballot(k[j] >= b3));
-        c2 += __popcll(ballot(k[j] >= b2));
-        c1 += __popcll(ballot(k[j] >= b1));
-      }
-      prefix = c3 >= P.top_k ? b3 : (c2 >= P.top_k ? b2 : (c1 >= P.top_k ? b1 : prefix));
-    }
-    cut = prefix;
-  }
-  int base = 0;
-#pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    const bool keep = k[j] != 0ull && k[j] >= cut;
-    const uint64_t b = ballot(keep);
-    const int pos = base + lanes_below(b);
-    if (keep && pos < 64) { L->k[pos] = k[j]; L->i[pos] = id[j]; }
-    base += __popcll(b);
-  }
-  E = base;
-  if (E > 64) return false;
-  // sentinels past the kept entries (key 0 is below every value, id above
-  // every id), so the unrolled scans below need no bounds tests
-  if (l < 8) { L->k[E + l] = 0ull; L->i[E + l] = INT_MAX; }
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   __builtin_amdgcn_wave_barrier();
-  // (1) rank = number of kept entries before this one; 8 entries per step
-  const uint64_t mk = l < E ? L->k[l] : 0ull;
-  const int32_t mi = l < E ? L->i[l] : INT_MAX;
-  int rank = 0;
-  for (int i = 0; i < E; i += 8) {
-    uint64_t ki[8];
-    int32_t ii[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) { ki[j] = L->k[i + j]; ii[j] = L->i[i + j]; }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) rank += (ki[j] > mk || (ki[j] == mk && ii[j] < mi)) ? 1 : 0;
-  }
-  if (l < E) { L->sk[rank] = mk; L->si[rank] = mi; }
-  if (l < 8) L->si[E + l] = INT_MAX;
-  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-  __builtin_amdgcn_wave_barrier();
+  const int E = min(nlist, 64);
   const uint64_t key = l < E ? L->sk[l] : 0ull;
   const int32_t idx = l < E ? L->si[l] : INT_MAX;
-  // (2) top-k: every record at or above the k-th largest value
+  const int32_t rid = l < E ? L->sr[l] : 0;
+  // (1) top-k: every entry at or above the k-th largest value
   int n = E;
-  if (P.top_k < E) {
-    const uint64_t kth = L->sk[P.top_k - 1];
+  if (P.top_k < nlist) {
+    const uint64_t kth = lane_read(key, P.top_k - 1);
     n = __popcll(ballot(l < E && key >= kth));
+    if (n == 64 && nlist > 64 && L->sk[64] == kth) return false;
   }
-  // (3) probabilities of the kept prefix; top-p on the unrenormalised vector
+  // (2) probabilities of the kept prefix; top-p on the unrenormalised vector
   const double Pj = l < n ? exp2(key2d(key) * kc - Rb) / S : 0.0;
   if (P.top_p < 1.0) {                                 // sampler.py:81-89
     const double cum = wave_scan_dpp(Pj);
@@ -715,28 +718,34 @@ __device__ inline bool lean_decide(const SampleArgs& A, int row, const cx_row_pa
     const uint64_t b = ballot(l < n && Pj < floor_p);
     if (b) n = __builtin_ctzll(b);
   }
-  // (4) normalise and draw in token-id order (sampler.py:123-127; choice ==
-  // searchsorted(cumsum / last, u, 'right')): F = mass of the kept records
-  // with an id <= this one
+  // (3) normalise and draw in token-id order (sampler.py:123-127; choice ==
+  // searchsorted(cumsum / last, u, 'right')): the kept mass goes to its id
+  // rank, lane l sums id ranks 4l .. 4l + 3, and a scan over the lanes gives
+  // the cumulative mass at every id rank
   const double qv = l < n ? Pj : 0.0;
   const double Z = wave_reduce(qv, OpAdd());
-  const double qi = qv / Z;
-  L->q[l] = qi;                                        // 0 past the kept prefix
-  if (l < 8) L->q[64 + l] = 0.0;
+  if (l < n) L->oq[rid] = qv / Z;
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   __builtin_amdgcn_wave_barrier();
-  double F = 0.0;
-  for (int i = 0; i < n; i += 8) {
-    int32_t ii[8];
-    double qq[8];
+  static_assert(LEAN_CAP == 4 * 64, "four id ranks per lane");
+  double f[4];
+  double run = 0.0;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) { ii[j] = L->si[i + j]; qq[j] = L->q[i + j]; }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) F += ii[j] <= idx ? qq[j] : 0.0;
+  for (int i = 0; i < 4; ++i) {
+    const int p = 4 * l + i;
+    run += p < nlist ? L->oq[p] : 0.0;
+    f[i] = run;
   }
-  const double last = wave_reduce(l < n ? F : 0.0, OpMax());
-  const int pick = wave_reduce((l < n && F / last > u) ? idx : INT_MAX, OpMin());
-  tok = pick != INT_MAX ? pick : wave_reduce(l < n ? idx : -1, OpMax());
+  const double incl = wave_scan_dpp(run);
+  double base = __shfl_up(incl, 1);
+  if (l == 0) base = 0.0;
+  const double last = lane_read(incl, 63);
+  int first = INT_MAX;
+#pragma unroll
+  for (int i = 3; i >= 0; --i)
+    if (4 * l + i < nlist && (base + f[i]) / last > u) first = 4 * l + i;
+  const uint64_t b = ballot(first != INT_MAX);
+  tok = b ? L->oid[lane_read(first, __builtin_ctzll(b))] : wave_reduce(l < n ? idx : -1, OpMax());
   return true;
 }
 
@@ -749,63 +758,80 @@ struct PenRec {
   int fl, pad;
 };
 
-// Wave w owns the 64-slot groups w, w + NWAVE, ... of the penalty index
-// once the index is built: after its stream it loads their raw logits,
-// computes their penalised values, the region pre-test copies and its share
-// of the penalty corrections to the sum.
-constexpr int GPW = NS_MAX / (64 * NWAVE);      // slot groups per wave at most
+// Wave w owns the dense entries w * 64 + lane + g * WG of the penalty index.
+// The raw logits of the first GD of them per lane are loaded before the
+// stream (they arrive while it runs); the rest, for windows with more than
+// GD * WG distinct ids, after it.
 
-// Issue the loads of the wave's owned ids' raw logits (to be consumed by
-// pen_correct after other work).
+// Byte offset of dense entry j's logit in the slice buffer `srs`, or the
+// buffer's end (a range-checked load there returns 0) past the list.
 template <bool BF16>
-__device__ __forceinline__ void pen_fetch(const PenIndex& X, const char* rowp,
-                                          float (&raw)[GPW]) {
-  using E = Elem<BF16>;
+__device__ __forceinline__ int dense_offset(const PenIndex& X, int j, int nd, int lo, int end) {
+  if (j >= nd) return end;
+  return (int)((X.hword[X.dense[j]] >> 12) - (uint32_t)lo) * (BF16 ? 2 : 4);
+}
+template <bool BF16>
+__device__ __forceinline__ float load_elem(__amdgpu_buffer_rsrc_t srs, int off) {
+  if constexpr (BF16)
+    return __uint_as_float((uint32_t)__builtin_amdgcn_raw_buffer_load_b16(srs, off, 0, 0) << 16);
+  else
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(srs, off, 0, 0));
+}
+
+// Visit the wave's dense entries: f(slot, hash word, raw logit).
+template <bool BF16, class F>
+__device__ __forceinline__ void for_dense(const PenIndex& X, int nd, const float (&rawd)[GD],
+                                          const char* rowp, F&& f) {
 #pragma unroll
-  for (int g = 0; g < GPW; ++g) {
-    const int s = (g * NWAVE + wave_id()) * 64 + lane_id();
-    const uint32_t hw = s < X.ns ? X.hword[s] : HW_EMPTY;
-    raw[g] = hw != HW_EMPTY ? E::scalar(rowp, (int)(hw >> 12)) : 0.0f;
+  for (int g = 0; g < GD; ++g) {
+    const int j = wave_id() * 64 + lane_id() + g * WG;
+    if (j < nd) {
+      const int slot = X.dense[j];
+      f(slot, X.hword[slot], rawd[g]);
+    }
+  }
+  for (int j = GD * WG + wave_id() * 64 + lane_id(); j < nd; j += WG) {
+    const int slot = X.dense[j];
+    const uint32_t hw = X.hword[slot];
+    f(slot, hw, Elem<BF16>::scalar(rowp, (int)(hw >> 12)));
   }
 }
 
-// The wave's penalty corrections: hval = raw logit, hpen = fp32(penalised
-// value), and against Rc = ceil(max * c) the sums of the raw terms (pr) and
-// of penalised minus raw terms (corr), fp32 terms each <= 1 and within TOL_T
-// of the exact ones.
-__device__ __forceinline__ void pen_correct(const PenIndex& X, const float (&raw)[GPW],
-                                            const cx_row_params& P, double kc, PenRec* rec) {
+// The wave's penalty corrections.  Pass 1 stores each id's raw logit in
+// hval, appends the penalised values at or above thr_w to the region list
+// and finds the largest value; pass 2 sums, against Rc = ceil(max * c), the
+// raw terms (pr) and the penalised-minus-raw terms (corr): fp32 terms each
+// <= 1 and within TOL_T of the exact ones.
+template <bool BF16>
+__device__ __forceinline__ void pen_correct(const PenIndex& X, int nd, const float (&rawd)[GD],
+                                            const char* rowp, const cx_row_params& P, double kc,
+                                            double thr_w, CX_LDS uint64_t* lgk,
+                                            CX_LDS int32_t* lgi, CX_LDS int* lcnt, PenRec* rec) {
   double pm = -__builtin_inf();
-  double xp[GPW];
-#pragma unroll
-  for (int g = 0; g < GPW; ++g) {
-    const int s = (g * NWAVE + wave_id()) * 64 + lane_id();
-    const uint32_t hw = s < X.ns ? X.hword[s] : HW_EMPTY;
-    xp[g] = 0.0;
-    if (hw == HW_EMPTY) continue;
-    xp[g] = penalise(raw[g], (int)(hw & 0xFFFu), P);
-    X.hval[s] = raw[g];
-    X.hpen[s] = (float)xp[g];
-    pm = (double)raw[g] > pm ? (double)raw[g] : pm;
-    pm = xp[g] > pm ? xp[g] : pm;
-  }
+  for_dense<BF16>(X, nd, rawd, rowp, [&](int slot, uint32_t hw, float raw) {
+    const double xp = penalise(raw, (int)(hw & 0xFFFu), P);
+    X.hval[slot] = raw;
+    pm = (double)raw > pm ? (double)raw : pm;
+    pm = xp > pm ? xp : pm;
+    if (xp >= thr_w) {
+      const int pos = __hip_atomic_fetch_add(lcnt, 1, CX_RELAXED_WG);
+      if (pos < LEAN_CAP) { lgk[pos] = d2key(xp); lgi[pos] = (int32_t)(hw >> 12); }
+    }
+  });
   pm = wave_reduce(pm, OpMax());
   // NaN / +-inf windows leave Rc at 0 (their rows go to the exact kernel)
   const double Rc = (pm > -__builtin_inf() && pm < __builtin_inf()) ? ceil(pm * kc) : 0.0;
   double corr = 0.0, pr = 0.0, pmx = -__builtin_inf();
   int fl = 0;
-#pragma unroll
-  for (int g = 0; g < GPW; ++g) {
-    const int s = (g * NWAVE + wave_id()) * 64 + lane_id();
-    const uint32_t hw = s < X.ns ? X.hword[s] : HW_EMPTY;
-    if (hw == HW_EMPTY) continue;
-    const double tr = (double)__builtin_amdgcn_exp2f((float)((double)raw[g] * kc - Rc));
-    const double tp = (double)__builtin_amdgcn_exp2f((float)(xp[g] * kc - Rc));
+  for_dense<BF16>(X, nd, rawd, rowp, [&](int slot, uint32_t hw, float raw) {
+    const double xp = penalise(raw, (int)(hw & 0xFFFu), P);
+    const double tr = (double)__builtin_amdgcn_exp2f((float)((double)raw * kc - Rc));
+    const double tp = (double)__builtin_amdgcn_exp2f((float)(xp * kc - Rc));
     pr += tr;
     corr += tp - tr;
-    if (xp[g] != xp[g]) fl = 1;
-    else pmx = xp[g] > pmx ? xp[g] : pmx;
-  }
+    if (xp != xp) fl = 1;
+    else pmx = xp > pmx ? xp : pmx;
+  });
   corr = wave_reduce(corr, OpAdd());
   pr = wave_reduce(pr, OpAdd());
   pmx = wave_reduce(pmx, OpMax());
@@ -828,7 +854,6 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   __shared__ float w_R[NWAVE];
   __shared__ uint32_t w_tau[NWAVE], w_kmx[NWAVE];
   __shared__ int w_fl[NWAVE];
-  __shared__ int s_done;
   __shared__ int w_cnt[NWAVE];
   __shared__ uint32_t s_shared;
   __shared__ uint32_t w_pub[NWAVE];
@@ -837,50 +862,28 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   __shared__ int s_cnt;
   __shared__ LeanLds s_lean;
 
+  __shared__ int s_nd;
   const int row = blockIdx.x / A.nsplit;
   const int split = blockIdx.x % A.nsplit;
   const int t = threadIdx.x;
-  // the row's parameters live in LDS after the first barrier (P), not in
-  // registers across the stream; P0 serves the prologue
-  __shared__ cx_row_params sP;
-  const cx_row_params P0 = sload_params(A.prm + row);
-  if (t == 0) sP = P0;
-  const double u_row = const_load(A.u + row);
-  const bool greedy = P0.temperature == 0.0;
   const int lo = split * A.split_len;
   const int hi = min(A.V, lo + A.split_len);
   const char* rowp = (const char*)A.logits + (size_t)row * (size_t)A.ld * (BF16 ? 2 : 4);
   const bool single = A.nsplit == 1;
-
-  int wlen = 0, wstart = 0;
-  if (A.ldh > 0) {
-    int len = max(0, min(const_load(A.hist_len + row), (int)A.ldh));
-    wstart = P0.n_keep > 0 ? max(0, len - max(64, P0.n_keep)) : 0;
-    wlen = len - wstart;
-  }
-  const bool pen_on = wlen > 0 && (P0.repetition_penalty != 1.0 || P0.presence_penalty != 0.0 ||
-                                   P0.frequency_penalty != 0.0);
   SplitStats* my = A.stats + (size_t)row * A.nsplit + split;
   Cand* mycand = A.cands + ((size_t)row * A.nsplit + split) * CAPS;
 
-  if (pen_on && wlen > WIN_MAX) {                    // window longer than the LDS index
-    if (t == 0) {
-      my->flags = SF_UNSUPPORTED; my->ncand = 0; my->tau = 1u;
-      my->m = 0; my->s = 0; my->tol = 0; my->best_i = INT_MAX; my->nan_i = INT_MAX;
-    }
-    if (single) write_row_result(A, row, CX_ROW_UNSUPPORTED, -1);
-    return;
-  }
-
-  // the window ids first, then this wave's first two chunks (wave_id and
-  // wave_id + NWAVE; the LDS counter hands out the rest from 2 * NWAVE on):
-  // all in flight while the index tables are cleared
-  // (all unconditional buffer loads, so waiting for the ids does not wait
-  // for the chunks)
+  // Vector loads first, before anything waits: the row's first HPT * WG
+  // history entries (where the window starts is known only with the
+  // parameters), then this wave's first two chunks (wave_id and wave_id +
+  // NWAVE; the LDS counter hands out the rest from 2 * NWAVE on).  All are
+  // unconditional range-checked buffer loads, so waiting for the ids does
+  // not wait for the chunks.
+  const bool has_hist = A.ldh > 0;
+  const int hcov = has_hist ? (int)min((int64_t)HPT * WG, A.ldh) : 0;
   const __amdgpu_buffer_rsrc_t hrs =
-      row_rsrc(pen_on ? (const void*)(A.hist + (size_t)row * A.ldh + wstart) : nullptr,
-               pen_on ? wlen * 4 : 0);
-  int32_t hid[HPT];                  // raw; entries at or past wlen are ignored
+      row_rsrc(has_hist ? (const void*)(A.hist + (size_t)row * A.ldh) : nullptr, hcov * 4);
+  int32_t hid[HPT];
 #pragma unroll
   for (int k = 0; k < HPT; ++k)
     hid[k] = (int)__builtin_amdgcn_raw_buffer_load_b32(hrs, (t + k * WG) * 4, 0, 0);
@@ -892,15 +895,41 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   load_chunk<BF16>(rs, ch0, q);
   load_chunk<BF16>(rs, ch0 + NWAVE, qn);
 
+  // the row's parameters live in LDS after the first barrier (P), not in
+  // registers across the stream; P0 serves the prologue
+  __shared__ cx_row_params sP;
+  const RowScalars RS = sload_row(A.prm + row, A.u + row,
+                                  has_hist ? A.hist_len + row : (const int32_t*)(A.u + row));
+  const cx_row_params& P0 = RS.p;
+  const double u_row = RS.u;
+  const bool greedy = P0.temperature == 0.0;
+  int wlen = 0, wstart = 0;
+  if (has_hist) {
+    const int len = max(0, min(RS.hlen, (int)A.ldh));
+    wstart = P0.n_keep > 0 ? max(0, len - max(64, P0.n_keep)) : 0;
+    wlen = len - wstart;
+  }
+  const bool pen_on = wlen > 0 && (P0.repetition_penalty != 1.0 || P0.presence_penalty != 0.0 ||
+                                   P0.frequency_penalty != 0.0);
+  if (pen_on && wlen > WIN_MAX) {                    // window longer than the LDS index
+    if (t == 0) {
+      my->flags = SF_UNSUPPORTED; my->ncand = 0; my->tau = 1u;
+      my->m = 0; my->s = 0; my->tol = 0; my->best_i = INT_MAX; my->nan_i = INT_MAX;
+    }
+    if (single) write_row_result(A, row, CX_ROW_UNSUPPORTED, -1);
+    return;
+  }
+
   PenIndex X;
   X.bitmap = to_lds((uint32_t*)(dyn + A.off_bitmap));
   X.hword = to_lds((uint32_t*)(dyn + A.off_hword));
   X.hval = to_lds((float*)(dyn + A.off_hval));
-  X.hpen = to_lds((float*)(dyn + A.off_hpen));
+  X.dense = to_lds((int32_t*)(dyn + A.off_dense));
   X.nbw = (hi - lo + 31) >> 5;
   X.ns = pen_on ? A.ns : 0;
   X.ns_log2 = A.ns_log2;
-  if (t == 0) { s_shared = 1u; s_chunk = 2 * NWAVE; s_cnt = 0; s_done = 0; }
+  if (t == 0) { sP = P0; s_shared = 1u; s_chunk = 2 * NWAVE; s_cnt = 0; s_nd = 0; }
+  if (t < LEAN_CAP) { s_lean.rv[t] = 0; s_lean.ri[t] = 0; }
   if (t < NWAVE) { w_pub[t] = 0u; w_cnt[t] = 0; }
   if (t < 4 * NWAVE) slots[t] = 0u;
   if (pen_on) {
@@ -909,18 +938,39 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   }
   __syncthreads();
   const cx_row_params& P = sP;
-  // index the window ids of this slice: a bitmap bit and a hash word
-  // (id << 12 | count) per distinct id
+  // index the window entries [wstart, wstart + wlen) whose ids fall in the
+  // slice: a bitmap bit and a hash word (id << 12 | count) per distinct id,
+  // whose slot its first inserter appends to the dense list
+  if (pen_on) {
+    const int wend = wstart + wlen;
+    auto index_id = [&](int id) {
+      if (id >= lo && id < hi) {
+        __hip_atomic_fetch_or(X.bitmap + ((id - lo) >> 5), 1u << ((id - lo) & 31), CX_RELAXED_WG);
+        bool created;
+        const int slot = pen_insert(X, id, created);
+        if (created) X.dense[__hip_atomic_fetch_add(to_lds(&s_nd), 1, CX_RELAXED_WG)] = slot;
+      }
+    };
 #pragma unroll
-  for (int k = 0; k < HPT; ++k) {
-    const int id = hid[k];
-    if (pen_on && t + k * WG < wlen && id >= lo && id < hi) {
-      __hip_atomic_fetch_or(X.bitmap + ((id - lo) >> 5), 1u << ((id - lo) & 31), CX_RELAXED_WG);
-      bool created;
-      pen_insert(X, id, created);
+    for (int k = 0; k < HPT; ++k) {
+      const int i = t + k * WG;
+      if (i >= wstart && i < wend) index_id(hid[k]);
     }
+    // windows reaching past the entries loaded up front
+    for (int i = max(wstart, HPT * WG) + t; i < wend; i += WG)
+      index_id(A.hist[(size_t)row * A.ldh + i]);
   }
   __syncthreads();
+  // the raw logits of this wave's first distinct ids, in flight during the
+  // stream (range-checked: past the list the loads return 0)
+  const int nd = pen_on ? s_nd : 0;
+  const int send = (hi - lo) * (BF16 ? 2 : 4);
+  const __amdgpu_buffer_rsrc_t srs = row_rsrc(rowp + (size_t)lo * (BF16 ? 2 : 4), send);
+  float rawd[GD];
+#pragma unroll
+  for (int g = 0; g < GD; ++g)
+    rawd[g] = load_elem<BF16>(srs, dense_offset<BF16>(X, wave_id() * 64 + lane_id() + g * WG, nd,
+                                                      lo, send));
   // ---------------------------------------------------------------- greedy
   if (greedy) {
     GreedyState gs{-__builtin_inff(), INT_MAX, INT_MAX};
@@ -928,15 +978,13 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
     double bv = gs.bi == INT_MAX ? -__builtin_inf() : (double)gs.bv;
     int bi = gs.bi;
     int ni = gs.nan_i;
-    // the window ids' penalised values (their raw logits fetched now)
-    for (int s = t; s < X.ns; s += WG) {
-      const uint32_t hw = X.hword[s];
-      if (hw == HW_EMPTY) continue;
+    // the window ids' penalised values
+    for_dense<BF16>(X, nd, rawd, rowp, [&](int, uint32_t hw, float raw) {
       const int id = (int)(hw >> 12);
-      const double xp = penalise(E::scalar(rowp, id), (int)(hw & 0xFFFu), P);
+      const double xp = penalise(raw, (int)(hw & 0xFFFu), P);
       if (xp != xp) ni = min(ni, id);
       else argmax_merge(bv, bi, xp, id);
-    }
+    });
     block_argmax(bv, bi, red_d, red_i);
     ni = block_min(ni, red_i, INT_MAX);
     if (single) {
@@ -989,14 +1037,21 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
       }
     }
   }
-  if (krow <= 64) publish_top(ck, NSLOT, lslots + NSLOT * wave_id());
-  else if (pub_r > 0) {
+  // The waves' first chunks together set the first threshold: for top-k
+  // rows (k <= 64) the k-th largest of the published lane values, for wider
+  // rows the smallest of the waves' r-th largest lane values.  (A wave's own
+  // lane values alone give a threshold too low to keep the first chunks'
+  // appends cheap.)
+  if (krow <= 64) {
+    publish_top(ck, NSLOT, lslots + NSLOT * wave_id());
+    __syncthreads();
+    raise_tau(wb, kth_of_lanes(lds_load(lslots + lane_id()), krow));
+  } else if (pub_r > 0) {
     const uint32_t th = kth_of_lanes(ck, pub_r);
     if (lane_id() == 0) lpub[wave_id()] = th;
+    __syncthreads();
+    raise_tau(wb, pub_min(lpub));
   }
-  __syncthreads();
-  if (krow <= 64) raise_tau(wb, kth_of_lanes(lds_load(lslots + lane_id()), krow));
-  else if (pub_r > 0) raise_tau(wb, pub_min(lpub));
 
   SState st{-__builtin_inff(), 3.402823466e38f, -__builtin_inff(), 0.0};
   uint64_t* gk = (uint64_t*)(dyn + A.off_gather);
@@ -1012,10 +1067,8 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   }
 
   // ---- per wave, after its stream: its region entries into the shared
-  // list (while its owned ids' raw logits are on the way), its penalty
-  // corrections, its sums and state for the combination
-  float raw[GPW];
-  if (pen_on) pen_fetch<BF16>(X, rowp, raw);
+  // list, its penalty corrections (with the penalised values at or above
+  // its threshold), its sums and state for the combination
   raise_tau(wb, lds_load(wb.shared));
   {
     const int n = wb.n;
@@ -1027,34 +1080,22 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
       }
     }
   }
-  if (pen_on) pen_correct(X, raw, P, kc, &s_pen[wave_id()]);
-  else if (lane_id() == 0) {
+  if (pen_on) {
+    pen_correct<BF16>(X, nd, rawd, rowp, P, kc, wb.tau <= 1u ? -__builtin_inf() : (double)wb.tauf,
+                      lgk, lgi, lcnt, &s_pen[wave_id()]);
+  } else if (lane_id() == 0) {
     s_pen[wave_id()].corr = 0.0; s_pen[wave_id()].pr = 0.0; s_pen[wave_id()].pmx = -__builtin_inf();
     s_pen[wave_id()].Rc = 0.0; s_pen[wave_id()].fl = 0;
-  }
-  {
-    // this wave's share of the window ids: penalised values at or above its
-    // threshold (fp32 pre-test, exact value for the survivors)
-    const float thr_f = wb.tauf;
-    const double thr_w = wb.tau <= 1u ? -__builtin_inf() : (double)wb.tauf;
-    for (int s = wave_id() * 64 + lane_id(); s < X.ns; s += NWAVE * 64) {
-      const uint32_t hw = X.hword[s];
-      if (hw == HW_EMPTY) continue;
-      // rounding is monotone: xp >= thr_f (a float) implies fp32(xp) >= thr_f
-      if (!(X.hpen[s] >= thr_f)) continue;
-      const double xp = penalise(X.hval[s], (int)(hw & 0xFFFu), P);
-      if (xp == xp && xp >= thr_w) {
-        const int pos = __hip_atomic_fetch_add(lcnt, 1, CX_RELAXED_WG);
-        if (pos < LEAN_CAP) { lgk[pos] = d2key(xp); lgi[pos] = (int32_t)(hw >> 12); }
-      }
-    }
   }
   const float Rw = wave_reduce(st.R, OpMax());
   double sl = st.s != 0.0 ? __builtin_ldexp(st.s, (int)fmaxf(st.R - Rw, -2048.0f)) : 0.0;
   sl = wave_reduce(sl, OpAdd());
   const uint32_t kmx_w = wave_reduce(ck, OpMax());
   const int fl = wave_reduce(st.s != st.s ? 1 : 0, OpOr());
-  if (krow <= 64) publish_top(ck, NSLOT, lslots + NSLOT * wave_id());
+  // Top-k rows the rank-parallel finish can take (static conditions).
+  const bool lean_static = single && P.top_k > 0 && P.top_k <= 64 && P.typical_p >= 1.0 &&
+                           !A.out_probs && A.logV * (1.0 / P.temperature) <= 740.0;
+  if (krow <= 64 && !lean_static) publish_top(ck, NSLOT, lslots + NSLOT * wave_id());
   if (lane_id() == 0) {
     w_s[wave_id()] = sl;
     w_R[wave_id()] = Rw;
@@ -1062,24 +1103,56 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
     w_kmx[wave_id()] = kmx_w;
     w_fl[wave_id()] = fl | (wb.overflow ? 2 : 0);
   }
-  // Top-k rows the one-wave finish can take (static conditions): the last
-  // wave to get here decides the row, the others are done.
-  const bool lean_static = single && P.top_k > 0 && P.top_k <= 64 && P.typical_p >= 1.0 &&
-                           !A.out_probs && A.logV * (1.0 / P.temperature) <= 740.0;
+  __syncthreads();
+  const int lw = lane_id() & 15;       // lane w of row 0 reads wave w's record
+
+  // ---- top-k finish: wave 0 combines the sums while the other waves rank
+  // the region list; then wave 0 decides.  A row it cannot decide (inexact
+  // sum, tie flood, long list, near a top-p boundary) is left pending for
+  // the exact kernel.
   if (lean_static) {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    int arrived = 0;
-    if (lane_id() == 0) arrived = __hip_atomic_fetch_add(to_lds(&s_done), 1, __ATOMIC_ACQ_REL,
-                                                         __HIP_MEMORY_SCOPE_WORKGROUP);
-    if (__builtin_amdgcn_readfirstlane(arrived) != NWAVE - 1) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-  } else {
+    CX_LDS LeanLds* const L = to_lds(&s_lean);
+    const int nlist = s_cnt;
+    const bool list_ok = nlist > 0 && nlist <= LEAN_CAP;
+    double Rb = 0.0, Ss = 0.0, tol = 0.0;
+    bool ok = false;
+    if (wave_id() == 0) {
+      // S = sum over waves of 2^(Rw - Rb) s_w + 2^(Rc_w - Rb) corr_w
+      const float Rl = w_R[lw];
+      const double Rcl = s_pen[lw].Rc;
+      const float Rf = row0_reduce(Rl, OpMax());
+      const int flw = row0_reduce(w_fl[lw] | s_pen[lw].fl, OpOr());
+      Rb = fmax((double)Rf, row0_reduce(Rcl, OpMax()));
+      // an exponent offset past +-2^22 leaves fp32 term arguments inexact
+      const bool rb_ok = Rf > -__builtin_inff() && fabs(Rb) < 4194304.0;
+      double PR = 0.0;
+      if (rb_ok) {
+        const double sw = w_s[lw];
+        const double cw = s_pen[lw].corr, pw = s_pen[lw].pr;
+        const int dc = (int)fmax(Rcl - Rb, -2048.0);
+        const double term =
+            (sw != 0.0 ? __builtin_ldexp(sw, (int)fmax((double)Rl - Rb, -2048.0)) : 0.0) +
+            (cw != 0.0 ? __builtin_ldexp(cw, dc) : 0.0);
+        Ss = row0_reduce(term, OpAdd());
+        PR = row0_reduce(pw != 0.0 ? __builtin_ldexp(pw, dc) : 0.0, OpAdd());
+      }
+      tol = TOL_S + 2.0 * TOL_T * PR / Ss;
+      ok = flw == 0 && rb_ok && Ss > 0.0 && Ss < __builtin_inf() && tol <= TOL_MAX && list_ok;
+    } else if (list_ok) {
+      lean_ranks(lgk, lgi, nlist, L);
+    }
     __syncthreads();
+    if (wave_id() != 0) return;
+    int tok = -1;
+    ok = ok && lean_decide(P, lgk, lgi, nlist, kc, Rb, Ss, tol, L, u_row, tok);
+    if (lane_id() == 0) {
+      A.out_id[row] = ok ? tok : -1;
+      A.row_status[row] = ok ? CX_ROW_OK : ROW_PENDING;
+    }
+    return;
   }
 
   // ---- combine: S = sum over waves of 2^(Rw - Rb) s_w + 2^(Rc_w - Rb) corr_w
-  // (lane w of row 0 reads wave w's record)
-  const int lw = lane_id() & 15;
   const float Rl = w_R[lw];
   const double Rcl = s_pen[lw].Rc;
   const float Rf = row0_reduce(Rl, OpMax());
@@ -1102,29 +1175,8 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
     Ss = row0_reduce(term, OpAdd());
     PR = row0_reduce(pw != 0.0 ? __builtin_ldexp(pw, dc) : 0.0, OpAdd());
   }
-  const double invT = 1.0 / P.temperature;
   const double tol = TOL_S + 2.0 * TOL_T * PR / Ss;
   const bool sum_ok = !anynan && rb_ok && Ss > 0.0 && Ss < __builtin_inf() && tol <= TOL_MAX;
-  const int nlist = s_cnt;
-
-  // ---- lean finish: this wave decides; a row it cannot decide (inexact
-  // sum, tie flood, long list, near a top-p boundary) is left pending for
-  // the exact kernel
-  if (lean_static) {
-    if (!(sum_ok && !ovf && nlist <= LEAN_CAP)) {
-      if (lane_id() == 0) { A.out_id[row] = -1; A.row_status[row] = ROW_PENDING; }
-      return;
-    }
-    const uint64_t thr64 = Tf <= 1u ? 1ull : d2key((double)key2f(Tf));
-    int tok = -1;
-    const bool ok = lean_decide(A, row, P, lgk, lgi, nlist, thr64, kc, Rb, Ss, tol,
-                                to_lds(&s_lean), u_row, tok);
-    if (lane_id() == 0) {
-      A.out_id[row] = ok ? tok : -1;
-      A.row_status[row] = ok ? CX_ROW_OK : ROW_PENDING;
-    }
-    return;
-  }
 
   // ---- general: bound the region, write it and the statistics, then finish
   if (wb.n > wb.kw) {
