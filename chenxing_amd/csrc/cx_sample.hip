@@ -643,13 +643,19 @@ struct LeanLds {
 // matter.  rv and ri start at zero.
 __device__ __forceinline__ void lean_ranks(const CX_LDS uint64_t* gk, const CX_LDS int32_t* gi,
                                            int nlist, CX_LDS LeanLds* L) {
+  static_assert(NWAVE == 16 && LEAN_CAP <= 256, "stripe layout");
+  // ng groups of 64 entries, per = 15 / ng stripes each; x / per as
+  // (x * ceil(2^16 / per)) >> 16, exact for x <= 15 * 256
   const int ng = (nlist + 63) >> 6;
-  const int per = (NWAVE - 1) / ng;
+  const int per = ng == 1 ? 15 : (ng == 2 ? 7 : (ng == 3 ? 5 : 3));
+  const uint32_t rcp = ng == 1 ? 4370u : (ng == 2 ? 9363u : (ng == 3 ? 13108u : 21846u));
   const int w = wave_id() - 1;
-  const int eg = w % ng, sp = w / ng;
+  const int sp = ng == 3 ? (int)(((uint32_t)w * 21846u) >> 16) : w >> (ng == 4 ? 2 : ng - 1);
+  const int eg = w - sp * ng;
   if (sp >= per) return;
   const int e = eg * 64 + lane_id();
-  const int j0 = sp * nlist / per, j1 = (sp + 1) * nlist / per;
+  const int j0 = (int)(((uint32_t)(sp * nlist) * rcp) >> 16);
+  const int j1 = (int)(((uint32_t)((sp + 1) * nlist) * rcp) >> 16);
   const uint64_t ke = e < nlist ? gk[e] : 0ull;
   const int32_t ie = e < nlist ? gi[e] : INT_MAX;
   int cv = 0, ci = 0;
@@ -875,10 +881,14 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
 
   // Vector loads first, before anything waits: the row's first HPT * WG
   // history entries (where the window starts is known only with the
-  // parameters), then this wave's first two chunks (wave_id and wave_id +
-  // NWAVE; the LDS counter hands out the rest from 2 * NWAVE on).  All are
-  // unconditional range-checked buffer loads, so waiting for the ids does
-  // not wait for the chunks.
+  // parameters), then this wave's first chunk (wave_id; its second,
+  // wave_id + NWAVE, follows after the first barrier, and the LDS counter
+  // hands out the rest from 2 * NWAVE on).  Every workgroup asks for its
+  // first chunks at once when the grid starts: holding the second ones back
+  // until the index tables are cleared halves that queue, and the ids and
+  // first chunks behind it arrive sooner.  All are unconditional
+  // range-checked buffer loads, so waiting for the ids does not wait for
+  // the chunks.
   const bool has_hist = A.ldh > 0;
   const int hcov = has_hist ? (int)min((int64_t)HPT * WG, A.ldh) : 0;
   const __amdgpu_buffer_rsrc_t hrs =
@@ -893,7 +903,6 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   const int ch0 = __builtin_amdgcn_readfirstlane(wave_id());
   typename E::V q[U], qn[U];
   load_chunk<BF16>(rs, ch0, q);
-  load_chunk<BF16>(rs, ch0 + NWAVE, qn);
 
   // the row's parameters live in LDS after the first barrier (P), not in
   // registers across the stream; P0 serves the prologue
@@ -937,6 +946,7 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
     for (int i = t; i < X.ns; i += WG) X.hword[i] = HW_EMPTY;
   }
   __syncthreads();
+  load_chunk<BF16>(rs, ch0 + NWAVE, qn);
   const cx_row_params& P = sP;
   // index the window entries [wstart, wstart + wlen) whose ids fall in the
   // slice: a bitmap bit and a hash word (id << 12 | count) per distinct id,
