@@ -92,6 +92,15 @@ constexpr int GD = 1;                           // distinct ids per thread whose
 __device__ __forceinline__ bool pen_bit(const PenIndex& X, int r) {
   return (X.bitmap[r >> 5] >> (r & 31)) & 1u;
 }
+// The NE penalty bits of the vector starting at slice offset r (a multiple
+// of NE, so they share one word), or 0 when !on.  The read is unconditional
+// (word 0 when !on) so it needs no branch.
+template <int NE>
+__device__ __forceinline__ uint32_t pen_bits(const PenIndex& X, bool on, int r) {
+  static_assert(32 % NE == 0, "a vector's bits in one word");
+  const uint32_t w = X.bitmap[on ? r >> 5 : 0];
+  return on ? (w >> (r & 31)) & ((1u << NE) - 1u) : 0u;
+}
 
 // Count one more occurrence of id; returns its slot, and in `created`
 // whether this call inserted it (one caller per distinct id).  Linear
@@ -1031,7 +1040,8 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   CX_LDS uint32_t* const lslots = to_lds(slots);
   CX_LDS uint32_t* const lpub = to_lds(w_pub);
 
-  // seed: every lane's largest unpenalised element of its first chunk
+  // seed: every lane's largest unpenalised element of its first chunk (a
+  // vector's NE penalty bits sit in one bitmap word: one LDS read each)
   uint32_t ck = 0u;
   if (wave_id() * CH < nv) {
 #pragma unroll
@@ -1039,9 +1049,10 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
       const int vi = wave_id() * CH + u * 64 + lane_id();
       float x[NE];
       E::unpack(q[u], x);
+      const uint32_t pb = pen_bits<NE>(X, pen_on && vi < nv, vi * NE);
 #pragma unroll
       for (int j = 0; j < NE; ++j) {
-        const bool ok = vi < nv && x[j] == x[j] && !(pen_on && pen_bit(X, vi * NE + j));
+        const bool ok = vi < nv && x[j] == x[j] && !((pb >> j) & 1u);
         const uint32_t k = ok ? f2key(x[j]) : 0u;
         ck = k > ck ? k : ck;
       }
