@@ -86,8 +86,6 @@ struct PenIndex {
 constexpr uint32_t HW_EMPTY = 0xFFFFFFFFu;
 constexpr int NSLOT = 4;                        // published lane keys per wave
 constexpr int HPT = (WIN_MAX + WG - 1) / WG;   // history entries per thread loaded up front
-constexpr int GD = 1;                           // distinct ids per thread whose raw logits
-                                                // are fetched before the stream
 
 __device__ __forceinline__ bool pen_bit(const PenIndex& X, int r) {
   return (X.bitmap[r >> 5] >> (r & 31)) & 1u;
@@ -773,82 +771,74 @@ struct PenRec {
   int fl, pad;
 };
 
-// Wave w owns the dense entries w * 64 + lane + g * WG of the penalty index.
-// The raw logits of the first GD of them per lane are loaded before the
-// stream (they arrive while it runs); the rest, for windows with more than
-// GD * WG distinct ids, after it.
+// The penalty work after the stream is shared out dynamically: waves take
+// 64-entry groups of the dense list from an LDS counter as their streams
+// end, so the waves that finish first do it and the last one usually finds
+// nothing left.
 
-// Byte offset of dense entry j's logit in the slice buffer `srs`, or the
-// buffer's end (a range-checked load there returns 0) past the list.
-template <bool BF16>
-__device__ __forceinline__ int dense_offset(const PenIndex& X, int j, int nd, int lo, int end) {
-  if (j >= nd) return end;
-  return (int)((X.hword[X.dense[j]] >> 12) - (uint32_t)lo) * (BF16 ? 2 : 4);
-}
-template <bool BF16>
-__device__ __forceinline__ float load_elem(__amdgpu_buffer_rsrc_t srs, int off) {
-  if constexpr (BF16)
-    return __uint_as_float((uint32_t)__builtin_amdgcn_raw_buffer_load_b16(srs, off, 0, 0) << 16);
-  else
-    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(srs, off, 0, 0));
+// Next group of the dense list for this wave, or -1 when none is left.
+__device__ __forceinline__ int next_group(CX_LDS int* ctr, int ngroups) {
+  int g = 0;
+  if (lane_id() == 0) g = __hip_atomic_fetch_add(ctr, 1, CX_RELAXED_WG);
+  g = __builtin_amdgcn_readfirstlane(g);
+  return g < ngroups ? g : -1;
 }
 
-// Visit the wave's dense entries: f(slot, hash word, raw logit).
-template <bool BF16, class F>
-__device__ __forceinline__ void for_dense(const PenIndex& X, int nd, const float (&rawd)[GD],
-                                          const char* rowp, F&& f) {
-#pragma unroll
-  for (int g = 0; g < GD; ++g) {
-    const int j = wave_id() * 64 + lane_id() + g * WG;
-    if (j < nd) {
-      const int slot = X.dense[j];
-      f(slot, X.hword[slot], rawd[g]);
-    }
-  }
-  for (int j = GD * WG + wave_id() * 64 + lane_id(); j < nd; j += WG) {
-    const int slot = X.dense[j];
-    const uint32_t hw = X.hword[slot];
-    f(slot, hw, Elem<BF16>::scalar(rowp, (int)(hw >> 12)));
-  }
-}
-
-// The wave's penalty corrections.  Pass 1 stores each id's raw logit in
-// hval, appends the penalised values at or above thr_w to the region list
-// and finds the largest value; pass 2 sums, against Rc = ceil(max * c), the
-// raw terms (pr) and the penalised-minus-raw terms (corr): fp32 terms each
-// <= 1 and within TOL_T of the exact ones.
+// The penalty corrections of the groups this wave takes.  Per group: each
+// id's raw logit into hval, its penalised value into the region list when
+// at or above thr_w, and, against the record's exponent Rc (the running
+// ceil(max * c), rescaled exactly when it rises), the raw terms (pr) and
+// the penalised-minus-raw terms (corr): fp32 terms each <= 1 and within
+// TOL_T of the exact ones.
 template <bool BF16>
-__device__ __forceinline__ void pen_correct(const PenIndex& X, int nd, const float (&rawd)[GD],
+__device__ __forceinline__ void pen_correct(const PenIndex& X, int nd, CX_LDS int* gctr,
                                             const char* rowp, const cx_row_params& P, double kc,
                                             double thr_w, CX_LDS uint64_t* lgk,
                                             CX_LDS int32_t* lgi, CX_LDS int* lcnt, PenRec* rec) {
-  double pm = -__builtin_inf();
-  for_dense<BF16>(X, nd, rawd, rowp, [&](int slot, uint32_t hw, float raw) {
-    const double xp = penalise(raw, (int)(hw & 0xFFFu), P);
-    X.hval[slot] = raw;
-    pm = (double)raw > pm ? (double)raw : pm;
-    pm = xp > pm ? xp : pm;
-    if (xp >= thr_w) {
-      const int pos = __hip_atomic_fetch_add(lcnt, 1, CX_RELAXED_WG);
-      if (pos < LEAN_CAP) { lgk[pos] = d2key(xp); lgi[pos] = (int32_t)(hw >> 12); }
-    }
-  });
-  pm = wave_reduce(pm, OpMax());
-  // NaN / +-inf windows leave Rc at 0 (their rows go to the exact kernel)
-  const double Rc = (pm > -__builtin_inf() && pm < __builtin_inf()) ? ceil(pm * kc) : 0.0;
-  double corr = 0.0, pr = 0.0, pmx = -__builtin_inf();
+  double corr = 0.0, pr = 0.0, pmx = -__builtin_inf(), Rc = 0.0;
   int fl = 0;
-  for_dense<BF16>(X, nd, rawd, rowp, [&](int slot, uint32_t hw, float raw) {
-    const double xp = penalise(raw, (int)(hw & 0xFFFu), P);
-    const double tr = (double)__builtin_amdgcn_exp2f((float)((double)raw * kc - Rc));
-    const double tp = (double)__builtin_amdgcn_exp2f((float)(xp * kc - Rc));
-    pr += tr;
-    corr += tp - tr;
-    if (xp != xp) fl = 1;
-    else pmx = xp > pmx ? xp : pmx;
-  });
-  corr = wave_reduce(corr, OpAdd());
-  pr = wave_reduce(pr, OpAdd());
+  bool any = false;
+  const int ngroups = (nd + 63) >> 6;
+  for (int g = next_group(gctr, ngroups); g >= 0; g = next_group(gctr, ngroups)) {
+    const int j = g * 64 + lane_id();
+    const bool v = j < nd;
+    const int slot = v ? X.dense[j] : 0;
+    const uint32_t hw = v ? X.hword[slot] : 0u;
+    const float raw = v ? Elem<BF16>::scalar(rowp, (int)(hw >> 12)) : 0.0f;
+    const double xp = v ? penalise(raw, (int)(hw & 0xFFFu), P) : -__builtin_inf();
+    double pm = -__builtin_inf();
+    if (v) {
+      X.hval[slot] = raw;
+      pm = (double)raw > pm ? (double)raw : pm;
+      pm = xp > pm ? xp : pm;
+      if (xp >= thr_w) {
+        const int pos = __hip_atomic_fetch_add(lcnt, 1, CX_RELAXED_WG);
+        if (pos < LEAN_CAP) { lgk[pos] = d2key(xp); lgi[pos] = (int32_t)(hw >> 12); }
+      }
+    }
+    pm = wave_reduce(pm, OpMax());
+    // NaN / +-inf windows leave the exponent at 0 (their rows go to the
+    // exact kernel)
+    const double Rg = (pm > -__builtin_inf() && pm < __builtin_inf()) ? ceil(pm * kc) : 0.0;
+    if (!any || Rg > Rc) {
+      if (any) {
+        const int d = (int)fmax(Rc - Rg, -2048.0);
+        corr = corr != 0.0 ? __builtin_ldexp(corr, d) : 0.0;
+        pr = pr != 0.0 ? __builtin_ldexp(pr, d) : 0.0;
+      }
+      Rc = Rg;
+      any = true;
+    }
+    double tr = 0.0, tp = 0.0;
+    if (v) {
+      tr = (double)__builtin_amdgcn_exp2f((float)((double)raw * kc - Rc));
+      tp = (double)__builtin_amdgcn_exp2f((float)(xp * kc - Rc));
+      if (xp != xp) fl = 1;
+      else pmx = xp > pmx ? xp : pmx;
+    }
+    corr += wave_reduce(tp - tr, OpAdd());
+    pr += wave_reduce(tr, OpAdd());
+  }
   pmx = wave_reduce(pmx, OpMax());
   fl = wave_reduce(fl, OpOr());
   if (lane_id() == 0) { rec->corr = corr; rec->pr = pr; rec->pmx = pmx; rec->Rc = Rc; rec->fl = fl; }
@@ -878,6 +868,7 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   __shared__ LeanLds s_lean;
 
   __shared__ int s_nd;
+  __shared__ int s_gctr;
   const int row = blockIdx.x / A.nsplit;
   const int split = blockIdx.x % A.nsplit;
   const int t = threadIdx.x;
@@ -946,7 +937,7 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   X.nbw = (hi - lo + 31) >> 5;
   X.ns = pen_on ? A.ns : 0;
   X.ns_log2 = A.ns_log2;
-  if (t == 0) { sP = P0; s_shared = 1u; s_chunk = 2 * NWAVE; s_cnt = 0; s_nd = 0; }
+  if (t == 0) { sP = P0; s_shared = 1u; s_chunk = 2 * NWAVE; s_cnt = 0; s_nd = 0; s_gctr = 0; }
   if (t < LEAN_CAP) { s_lean.rv[t] = 0; s_lean.ri[t] = 0; }
   if (t < NWAVE) { w_pub[t] = 0u; w_cnt[t] = 0; }
   if (t < 4 * NWAVE) slots[t] = 0u;
@@ -980,16 +971,8 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
       index_id(A.hist[(size_t)row * A.ldh + i]);
   }
   __syncthreads();
-  // the raw logits of this wave's first distinct ids, in flight during the
-  // stream (range-checked: past the list the loads return 0)
   const int nd = pen_on ? s_nd : 0;
-  const int send = (hi - lo) * (BF16 ? 2 : 4);
-  const __amdgpu_buffer_rsrc_t srs = row_rsrc(rowp + (size_t)lo * (BF16 ? 2 : 4), send);
-  float rawd[GD];
-#pragma unroll
-  for (int g = 0; g < GD; ++g)
-    rawd[g] = load_elem<BF16>(srs, dense_offset<BF16>(X, wave_id() * 64 + lane_id() + g * WG, nd,
-                                                      lo, send));
+  CX_LDS int* const gctr = to_lds(&s_gctr);
   // ---------------------------------------------------------------- greedy
   if (greedy) {
     GreedyState gs{-__builtin_inff(), INT_MAX, INT_MAX};
@@ -997,13 +980,19 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
     double bv = gs.bi == INT_MAX ? -__builtin_inf() : (double)gs.bv;
     int bi = gs.bi;
     int ni = gs.nan_i;
-    // the window ids' penalised values
-    for_dense<BF16>(X, nd, rawd, rowp, [&](int, uint32_t hw, float raw) {
-      const int id = (int)(hw >> 12);
-      const double xp = penalise(raw, (int)(hw & 0xFFFu), P);
-      if (xp != xp) ni = min(ni, id);
-      else argmax_merge(bv, bi, xp, id);
-    });
+    // the window ids' penalised values (groups of the dense list, taken as
+    // the waves' streams end)
+    const int ngroups = (nd + 63) >> 6;
+    for (int g = next_group(gctr, ngroups); g >= 0; g = next_group(gctr, ngroups)) {
+      const int j = g * 64 + lane_id();
+      if (j < nd) {
+        const uint32_t hw = X.hword[X.dense[j]];
+        const int id = (int)(hw >> 12);
+        const double xp = penalise(E::scalar(rowp, id), (int)(hw & 0xFFFu), P);
+        if (xp != xp) ni = min(ni, id);
+        else argmax_merge(bv, bi, xp, id);
+      }
+    }
     block_argmax(bv, bi, red_d, red_i);
     ni = block_min(ni, red_i, INT_MAX);
     if (single) {
@@ -1102,7 +1091,7 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
     }
   }
   if (pen_on) {
-    pen_correct<BF16>(X, nd, rawd, rowp, P, kc, wb.tau <= 1u ? -__builtin_inf() : (double)wb.tauf,
+    pen_correct<BF16>(X, nd, gctr, rowp, P, kc, wb.tau <= 1u ? -__builtin_inf() : (double)wb.tauf,
                       lgk, lgi, lcnt, &s_pen[wave_id()]);
   } else if (lane_id() == 0) {
     s_pen[wave_id()].corr = 0.0; s_pen[wave_id()].pr = 0.0; s_pen[wave_id()].pmx = -__builtin_inf();
