@@ -290,6 +290,107 @@ __device__ bool select_prefix(const SlowRow& R, const Filters& F, const Cut& eli
   return true;
 }
 
+// Bucket of value v in the linear split of [lo, lo + NB / inv): monotone in
+// v, clamped to [0, NB).
+__device__ __forceinline__ int lin_bucket(double v, double lo, double inv) {
+  const double f = (v - lo) * inv;
+  return f < 0.0 ? 0 : (f >= (double)(NB - 1) ? NB - 1 : (int)f);
+}
+
+// Top-p over a logit row with no top-k before it (sampler.py:81-89): the
+// shortest prefix in (value desc, idx asc) order holding `target` mass.
+// Level 0 splits the values in [vlo, M] linearly into NB buckets (values far
+// apart land in different buckets, so the mass atomics rarely collide); a
+// level keeps the bucket the cut falls in and splits it again, and a bucket
+// of at most SCAP elements is gathered, sorted and scanned.  Every level
+// classifies an element by the same chain of bucket tests, so "above",
+// "in" and "below" stay consistent across the passes.  Returns false when
+// this cannot decide -- the elements at or above vlo hold less than the
+// target, or MAXLV levels leave a bucket larger than SCAP -- and the
+// caller then runs select_prefix.  tsum: WG doubles of LDS.
+__device__ bool select_mass_linear(const SlowRow& R, double target, double vlo, SlowLds& L,
+                                   double* tsum, Cut& out, double* red_d, int* red_i) {
+  static_assert(NB == WG, "one bucket per thread");
+  constexpr int MAXLV = 4;
+  const int t = threadIdx.x;
+  double lo[MAXLV], inv[MAXLV];
+  int bs[MAXLV];
+  if (!(R.M > vlo)) return false;
+  lo[0] = vlo;
+  inv[0] = (double)NB / (R.M - vlo);
+  double above = 0.0;
+  for (int lv = 0; lv < MAXLV; ++lv) {
+    L.cnt[t] = 0u;
+    L.mass[t] = 0.0;
+    __syncthreads();
+#pragma unroll 4
+    for (int i = t; i < R.V; i += WG) {
+      const double v = value_at(R, i);
+      if (!(v >= vlo)) continue;
+      bool in = true;
+      for (int m = 0; m < lv; ++m)
+        if (lin_bucket(v, lo[m], inv[m]) != bs[m]) { in = false; break; }
+      if (!in) continue;
+      const int b = lin_bucket(v, lo[lv], inv[lv]);
+      atomicAdd(&L.cnt[b], 1u);
+      atomicAdd(&L.mass[b], mass_of(R, v));
+    }
+    __syncthreads();
+    // suffix masses: tsum[NB-1-b] = mass[b], inclusive scan
+    const uint32_t cb = L.cnt[t];
+    const double mb = L.mass[t];
+    tsum[NB - 1 - t] = mb;
+    __syncthreads();
+    block_scan(tsum, NB, red_d);
+    const double suf = tsum[NB - 1 - t];             // sum over buckets >= t
+    // the cut's bucket: the highest non-empty bucket whose suffix reaches
+    // the target (suffix masses only grow toward lower buckets)
+    const int cand = (cb > 0u && above + suf >= target) ? t : -1;
+    const int bstar = block_max(cand, red_i, -1);
+    if (bstar < 0) return false;
+    const double above_b = above + (bstar + 1 < NB ? tsum[NB - 2 - bstar] : 0.0);
+    const int nb = (int)L.cnt[bstar];
+    __syncthreads();
+    if (nb <= SCAP) {
+      __shared__ int gn;
+      if (t == 0) gn = 0;
+      __syncthreads();
+      for (int i = t; i < R.V; i += WG) {
+        const double v = value_at(R, i);
+        if (!(v >= vlo)) continue;
+        bool in = true;
+        for (int m = 0; m < lv; ++m)
+          if (lin_bucket(v, lo[m], inv[m]) != bs[m]) { in = false; break; }
+        if (!in || lin_bucket(v, lo[lv], inv[lv]) != bstar) continue;
+        const int pos = atomicAdd(&gn, 1);
+        if (pos < SCAP) { L.gk[pos] = d2key(v); L.gi[pos] = i; L.gm[pos] = mass_of(R, v); }
+      }
+      __syncthreads();
+      const int n = min(gn, SCAP);
+      for (int j = t; j < n; j += WG) L.ga[j] = j;
+      __syncthreads();
+      block_sort(L.gk, L.gi, L.ga, n);
+      // masses in sorted order, their prefix sums, and the first position
+      // where the running total reaches the target (the last if none does)
+      tsum[t] = t < n ? L.gm[L.ga[t]] : 0.0;
+      __syncthreads();
+      block_scan(tsum, NB, red_d);
+      const int hit = (t < n && (above_b + tsum[t] >= target || t == n - 1)) ? t : INT_MAX;
+      const int j = block_min(hit, red_i, INT_MAX);
+      out.k = L.gk[j];
+      out.i = L.gi[j];
+      __syncthreads();
+      return true;
+    }
+    if (lv + 1 == MAXLV) return false;
+    bs[lv] = bstar;
+    lo[lv + 1] = lo[lv] + (double)bstar / inv[lv];
+    inv[lv + 1] = inv[lv] * (double)NB;
+    above = above_b;
+  }
+  return false;
+}
+
 // Row reader and penalty tables of one row (all WG threads; ends with a
 // __syncthreads when tables are built).  The window is the last
 // max(64, n_keep) history ids if n_keep > 0, else all of them
@@ -462,9 +563,20 @@ __device__ inline void slow_row(const SampleArgs& A, int row, unsigned char* dyn
   }
   if (P.top_p < 1.0) {                                       // sampler.py:81-89
     Cut c;
-    const uint64_t lo = F.rank.k > kmin ? F.rank.k : kmin;
-    if (select_prefix<false, true>(R, F, F.rank, P.top_p, lo, kmax, L, c, red_d, red_i))
-      F.rank = c;
+    // without top-k: linear value buckets from vlo, below which the row
+    // holds under a quarter of the mass outside the nucleus
+    // (V exp((vlo - M) / T) / S = (1 - top_p) / 4)
+    bool done = false;
+    if (F.rank.k == 0ull) {
+      const double vlo = fmax(mn, mx + P.temperature * log(0.25 * (1.0 - P.top_p) * R.S / (double)V));
+      done = select_mass_linear(R, P.top_p, vlo, L, tsum, c, red_d, red_i);
+      if (done) F.rank = c;
+    }
+    if (!done) {
+      const uint64_t lo = F.rank.k > kmin ? F.rank.k : kmin;
+      if (select_prefix<false, true>(R, F, F.rank, P.top_p, lo, kmax, L, c, red_d, red_i))
+        F.rank = c;
+    }
   }
   if (P.min_p > 0.0) F.floor_p = P.min_p * (1.0 / R.S);      // sampler.py:91-93
   if (P.typical_p < 1.0) {                                   // sampler.py:95-105
