@@ -88,7 +88,11 @@ class DeviceVerify:
 
     def __call__(self):
         from chenxing_amd import _lib
-        _lib.spec_verify_device(self.t, self.d, self.ids, self.u, self.T, *self.out)
+        # a batch with every temperature 0 needs no draft logits (greedy verify
+        # compares target argmaxes with the proposals); without them the
+        # stochastic stages are not launched, as in the host variant
+        draft = None if not np.any(self.w.temperature) else self.d
+        _lib.spec_verify_device(self.t, draft, self.ids, self.u, self.T, *self.out)
 
 
 def time_steps(fn, steps: int, warmup: int, kernel: int):

@@ -105,6 +105,7 @@ static_assert(sizeof(ChunkStats) == 32, "ChunkStats layout");
 static_assert(sizeof(SeqState) == 64, "SeqState layout");
 
 constexpr int SUB = 512;               // elements per normaliser partial: one wave, 8 per lane
+constexpr int NORM_WGS = 8;             // verify_norm workgroups per sequence
 constexpr int AMB_CAP = 8;             // undecided residual signs kept per partial
 
 // Exact normaliser partials of the rejected position's row pair over one

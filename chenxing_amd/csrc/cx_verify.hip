@@ -17,8 +17,9 @@
 //                     min/max semantics; a test whose ratio lies within the
 //                     normalisers' error bound of its uniform is re-decided
 //                     with exact fp64 normalisers.
-//   3. verify_norm    one wave per 512-element sub-chunk of the row pair at
-//                     the rejected position r: exact fp64 normaliser
+//   3. verify_norm    NORM_WGS workgroups per sequence, each wave looping over
+//                     512-element sub-chunks of the row pair at the rejected
+//                     position r (the next one's loads in flight): exact fp64 normaliser
 //                     partials of p and q, and the residual max(p - q, 0)
 //                     split into elements whose sign is sure (summed) and the
 //                     few that are not (listed).
@@ -451,14 +452,11 @@ __device__ __forceinline__ void pair_terms(const float (&xt)[8], const float (&x
 // One wave per 512-element sub-chunk of the rejected row pair.
 __global__ __launch_bounds__(WG) void verify_norm(VerifyArgs A) {
   __shared__ double tab[64];
-  const int per_b = (A.nsub + NWAVE - 1) / NWAVE;
-  const int b = blockIdx.x / per_b;
+  const int b = blockIdx.x / NORM_WGS;
   const float T = A.temperature[b];
   const SeqState q = A.seq[b];
   if (T == 0.0f || q.rej1 == 0) return;
   load_exp64_tab(tab);
-  const int sub = (blockIdx.x % per_b) * NWAVE + wave_id();
-  if (sub >= A.nsub) return;
   const int r = q.rej1 - 1;
   const float* tr = trow(A, b, r);
   const float* dr = drow(A, b, r);
@@ -467,49 +465,61 @@ __global__ __launch_bounds__(WG) void verify_norm(VerifyArgs A) {
   const double lam0 = q.St / q.Sq;
   const double eps = sign_margin(q, T);
   const int l = lane_id();
-  const int e0 = sub * SUB + l * 8;
+  // this wave's sub-chunks: sub0, sub0 + stride, ...; the next one's loads
+  // are issued before the current one is reduced
+  const int stride = NORM_WGS * NWAVE;
+  int sub = (blockIdx.x % NORM_WGS) * NWAVE + wave_id();
   float xt[8], xq[8];
-  load8(tr, e0, A.V, xt);
-  load8(dr, e0, A.V, xq);
-  double ev[8], fv[8];
-  if (T == 1.0f) pair_terms<true>(xt, xq, e0, A.V, invT, zmt, zmq, tab, ev, fv);
-  else pair_terms<false>(xt, xq, e0, A.V, invT, zmt, zmq, tab, ev, fv);
-  double se = 0.0, sf = 0.0, dp = 0.0, fp = 0.0;
-  unsigned amb = 0;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const double e = ev[j], f = fv[j];
-    se += e;
-    sf += f;
-    const double lf = lam0 * f;
-    const bool pos = e > lf * (1.0 + eps);
-    dp += pos ? e - lf : 0.0;
-    fp += pos ? f : 0.0;
-    amb |= (!pos && e >= lf * (1.0 - eps) && (e != 0.0 || f != 0.0)) ? 1u << j : 0u;
+  if (sub < A.nsub) {
+    load8(tr, sub * SUB + l * 8, A.V, xt);
+    load8(dr, sub * SUB + l * 8, A.V, xq);
   }
-  se = wave_reduce(se, OpAdd());
-  sf = wave_reduce(sf, OpAdd());
-  dp = wave_reduce(dp, OpAdd());
-  fp = wave_reduce(fp, OpAdd());
-  const size_t part = (size_t)b * A.nsub + sub;
-  int namb = 0;
-  if (__ballot(amb != 0)) {                           // rare: list the undecided signs
-    AmbEntry* out = A.amb + part * AMB_CAP;
+  for (; sub < A.nsub; sub += stride) {
+    const int e0 = sub * SUB + l * 8;
+    double ev[8], fv[8];
+    if (T == 1.0f) pair_terms<true>(xt, xq, e0, A.V, invT, zmt, zmq, tab, ev, fv);
+    else pair_terms<false>(xt, xq, e0, A.V, invT, zmt, zmq, tab, ev, fv);
+    if (sub + stride < A.nsub) {
+      load8(tr, (sub + stride) * SUB + l * 8, A.V, xt);
+      load8(dr, (sub + stride) * SUB + l * 8, A.V, xq);
+    }
+    double se = 0.0, sf = 0.0, dp = 0.0, fp = 0.0;
+    unsigned amb = 0;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const bool a = (amb >> j) & 1u;
-      const uint64_t m = __ballot(a);
-      const int idx = namb + lanes_below(m);
-      if (a && idx < AMB_CAP) { out[idx].e = ev[j]; out[idx].f = fv[j]; }
-      namb += __builtin_popcountll(m);
+      const double e = ev[j], f = fv[j];
+      se += e;
+      sf += f;
+      const double lf = lam0 * f;
+      const bool pos = e > lf * (1.0 + eps);
+      dp += pos ? e - lf : 0.0;
+      fp += pos ? f : 0.0;
+      amb |= (!pos && e >= lf * (1.0 - eps) && (e != 0.0 || f != 0.0)) ? 1u << j : 0u;
     }
-  }
-  if (l == 0) {
-    NormPart P;
-    P.se = se; P.sf = sf; P.dp = dp; P.fp = fp;
-    P.namb = namb;
-    for (int k = 0; k < 7; ++k) P.pad[k] = 0;
-    A.npart[part] = P;
+    se = wave_reduce(se, OpAdd());
+    sf = wave_reduce(sf, OpAdd());
+    dp = wave_reduce(dp, OpAdd());
+    fp = wave_reduce(fp, OpAdd());
+    const size_t part = (size_t)b * A.nsub + sub;
+    int namb = 0;
+    if (__ballot(amb != 0)) {                         // rare: list the undecided signs
+      AmbEntry* out = A.amb + part * AMB_CAP;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const bool a = (amb >> j) & 1u;
+        const uint64_t m = __ballot(a);
+        const int idx = namb + lanes_below(m);
+        if (a && idx < AMB_CAP) { out[idx].e = ev[j]; out[idx].f = fv[j]; }
+        namb += __builtin_popcountll(m);
+      }
+    }
+    if (l == 0) {
+      NormPart P;
+      P.se = se; P.sf = sf; P.dp = dp; P.fp = fp;
+      P.namb = namb;
+      for (int k = 0; k < 7; ++k) P.pad[k] = 0;
+      A.npart[part] = P;
+    }
   }
 }
 
@@ -670,8 +680,7 @@ int launch_verify(const VerifyArgs& A, bool any_stochastic, hipStream_t s) {
   timed_launch(CX_KERNEL_VERIFY_STATS, verify_stats, dim3(nrows * per_row), dim3(WG), 0, s, A);
   timed_launch(CX_KERNEL_VERIFY_REST, verify_decide, dim3(A.B), dim3(WG), 0, s, A);
   if (any_stochastic) {
-    const int per_b = (A.nsub + NWAVE - 1) / NWAVE;
-    timed_launch(CX_KERNEL_VERIFY_REST, verify_norm, dim3(A.B * per_b), dim3(WG), 0, s, A);
+    timed_launch(CX_KERNEL_VERIFY_REST, verify_norm, dim3(A.B * NORM_WGS), dim3(WG), 0, s, A);
     timed_launch(CX_KERNEL_VERIFY_REST, verify_draw, dim3(A.B), dim3(WG), 0, s, A);
   }
   return (int)hipGetLastError();
