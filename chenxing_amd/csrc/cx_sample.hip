@@ -191,8 +191,10 @@ __device__ __forceinline__ int next_chunk(CX_LDS int* counter) {
 }
 
 // The k-th largest of the 64 lane values (1 <= k <= 64): two key bits per
-// step, three independent ballot counts each.
-__device__ __noinline__ uint32_t kth_of_lanes(uint32_t v, int k) {
+// step, three independent ballot counts each.  Inlined: a call makes the
+// callee wait for every load in flight (the calling convention), which in
+// the stream would drain the wave's chunk pipeline.
+__device__ __forceinline__ uint32_t kth_of_lanes(uint32_t v, int k) {
   uint32_t prefix = 0u;
   for (int sh = 30; sh >= 0; sh -= 2) {
     const uint32_t b1 = prefix | (1u << sh), b2 = prefix | (2u << sh), b3 = prefix | (3u << sh);
