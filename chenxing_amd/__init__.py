@@ -7,7 +7,8 @@ host side with the reference's call signatures.
 """
 from .params import SamplingParams, RowParams
 
-__all__ = ["SamplingParams", "RowParams", "Sampler", "SpeculativeDecoder"]
+__all__ = ["SamplingParams", "RowParams", "Sampler", "SpeculativeDecoder",
+           "decode_step_batched", "scheduler_step_batched"]
 
 
 def __getattr__(name):
@@ -17,4 +18,7 @@ def __getattr__(name):
     if name == "SpeculativeDecoder":
         from .speculative import SpeculativeDecoder
         return SpeculativeDecoder
+    if name in ("decode_step_batched", "scheduler_step_batched"):
+        from . import decode
+        return getattr(decode, name)
     raise AttributeError(name)

@@ -147,7 +147,8 @@ class Sampler:
         Equivalent to ``[self.sample(logits[b], params[b], generated_ids[b])
         for b in range(B)]``, including the order in which rows draw from
         the sampler's generator and the exception the first failing row
-        raises.  ``logits`` is a numpy array (float32 or float64) or a CUDA
+        raises (its ``tokens_before`` attribute holds the tokens of the rows
+        before it).  ``logits`` is a numpy array (float32 or float64) or a CUDA
         tensor (float32, bfloat16 or float64) that stays on the device.
         """
         on_dev = _is_torch_cuda(logits)
@@ -204,12 +205,18 @@ class Sampler:
             self._rng.bit_generator.state = state
             for b in range(B):
                 code = int(st[b]) & 0xFF
+                err = None
                 if code == _lib.ROW_OK and V != self.vocab_size:
-                    raise ValueError(_NUMPY_SIZE)      # choice(vocab_size, p) (:127)
-                if code == _lib.ROW_ERROR:
-                    raise ValueError(_NUMPY_NAN)
-                if code == _lib.ROW_UNSUPPORTED:
-                    raise ValueError("row outside the sampler library's limits")
+                    err = ValueError(_NUMPY_SIZE)      # choice(vocab_size, p) (:127)
+                elif code == _lib.ROW_ERROR:
+                    err = ValueError(_NUMPY_NAN)
+                elif code == _lib.ROW_UNSUPPORTED:
+                    err = ValueError("row outside the sampler library's limits")
+                if err is not None:
+                    # the tokens of the rows before it, which the per-row
+                    # loop would have returned before raising
+                    err.tokens_before = out
+                    raise err
                 if code == _lib.ROW_OK and seeds[b] is None:
                     self._rng.random()                 # the variate this row drew
                 out.append(int(ids[b]))
