@@ -521,13 +521,15 @@ __device__ __forceinline__ void stream_stoch(__amdgpu_buffer_rsrc_t rs,
       append_chunk<BF16>(wb, x, flagged, vb, nv, lo, pen_on, X, share, ck);
       fresh = true;
     }
+    const int cnn = cn < nch ? __builtin_amdgcn_readfirstlane(next_chunk(chunk_ctr)) : nch;
+    load_chunk<BF16>(rs, cnn, b);      // past the slice: zeros, never consumed
+    // after the refill, so both chunks are in flight while the wave
+    // publishes (a publish is a few hundred instructions)
     if ((it == 1 || it == 3) && fresh) {
       publish(ck, krow, pub_r, slots, w_pub, wb.shared);
       raise_tau(wb, lds_load(wb.shared));
       fresh = false;
     }
-    const int cnn = cn < nch ? __builtin_amdgcn_readfirstlane(next_chunk(chunk_ctr)) : nch;
-    load_chunk<BF16>(rs, cnn, b);      // past the slice: zeros, never consumed
     ch = cn;
     cn = cnn;
     ++it;
