@@ -23,10 +23,12 @@
 //                     partials of p and q, and the residual max(p - q, 0)
 //                     split into elements whose sign is sure (summed) and the
 //                     few that are not (listed).
-//   4. verify_draw    grid B: exact normalisers, the residual mass of every
-//                     sub-chunk from the partials, the sub-chunk holding
-//                     u * R, and a scan of it; a draw within 1e-12 (relative)
-//                     of a step is redone over the whole row pair.
+//   4. verify_draw    grid B: wave 0 alone sums the exact normalisers, scans
+//                     the residual mass of every sub-chunk from the partials,
+//                     finds the sub-chunk holding u * R and scans its 512
+//                     elements with wave-level prefix sums, with no block
+//                     barrier; a draw within 1e-12 (relative) of a step is
+//                     redone by the whole workgroup over the whole row pair.
 //
 // fp64 terms use exp64 (table-driven, within 1 ulp) of fl32(x / T), the
 // reference's fp32 quotient (div32).
@@ -533,8 +535,8 @@ __global__ __launch_bounds__(WG) void verify_draw(VerifyArgs A) {
   __shared__ int red_i[2 * NWAVE + 4];
   __shared__ double tab[64];
   __shared__ double tsum[2 * WG];
-  __shared__ int s_over[64];
-  __shared__ int s_nover;
+  __shared__ double s_lam[3];
+  __shared__ int s_state[2];                          // {0 undecided, 1 token, 2 NaN}, token
   const int b = blockIdx.x;
   const int t = threadIdx.x;
   const float T = A.temperature[b];
@@ -548,63 +550,114 @@ __global__ __launch_bounds__(WG) void verify_draw(VerifyArgs A) {
   const float* dr = drow(A, b, r);
   const double u = A.u[(size_t)b * (g + 1) + r + 1];
   const NormPart* np = A.npart + (size_t)b * ns;
-  // this thread's sub-chunks 2t and 2t + 1
-  NormPart P[2];
-#pragma unroll
-  for (int k = 0; k < 2; ++k) {
-    const int sidx = 2 * t + k;
-    if (sidx < ns) P[k] = np[sidx];
-    else { P[k].se = P[k].sf = P[k].dp = P[k].fp = 0.0; P[k].namb = 0; }
-  }
-  if (t == 0) s_nover = 0;
-  // exact normalisers (fixed reduction order)
-  const double St = block_sum(P[0].se + P[1].se, red_d);
-  const double Sq = block_sum(P[0].sf + P[1].sf, red_d);
-  const double lam = St / Sq, lam0 = q.St / q.Sq;
   ResidCtx C;
   C.invT = 1.0 / (double)T;
   C.zmt = q.Mt / T;
   C.zmq = q.Mq / T;
-  C.invSt = 1.0 / St;
-  C.invSq = 1.0 / Sq;
   C.tab = tab;
-  // residual mass of each sub-chunk: the sure-positive part and the list
-#pragma unroll
-  for (int k = 0; k < 2; ++k) {
-    const int sidx = 2 * t + k;
-    double w = 0.0;
-    if (sidx < ns) {
-      if (P[k].namb > AMB_CAP) {
-        const int o = atomicAdd(&s_nover, 1);
-        if (o < 64) s_over[o] = sidx;
+  const double err = 1e-12;                           // relative rounding of the sums
+  // Wave 0 decides from the partials (lane-strided sums and wave scans, no
+  // block barriers): the exact normalisers, every sub-chunk's residual mass,
+  // the sub-chunk holding u * W and, scanned in id order, the element in it.
+  // A draw within err of a step, a list that overflowed, W too small or NaN
+  // leave the row to the block-wide exact redo below.
+  if (wave_id() == 0) {
+    const int l = lane_id();
+    double st = 0.0, sq = 0.0;
+    for (int s = l; s < ns; s += 64) { st += np[s].se; sq += np[s].sf; }
+    const double St = wave_reduce(st, OpAdd()), Sq = wave_reduce(sq, OpAdd());
+    const double lam = St / Sq, lam0 = q.St / q.Sq;
+    // residual mass of each sub-chunk: the sure-positive part and the list
+    bool over = false;
+    for (int s = l; s < ns; s += 64) {
+      const NormPart P = np[s];
+      double w = 0.0;
+      if (P.namb > AMB_CAP) {
+        over = true;
       } else {
-        w = P[k].dp - (lam - lam0) * P[k].fp;
-        const AmbEntry* am = A.amb + ((size_t)b * ns + sidx) * AMB_CAP;
-        for (int j = 0; j < P[k].namb; ++j) {
+        w = P.dp - (lam - lam0) * P.fp;
+        const AmbEntry* am = A.amb + ((size_t)b * ns + s) * AMB_CAP;
+        for (int j = 0; j < P.namb; ++j) {
           const double d = am[j].e - lam * am[j].f;
           w += d > 0.0 ? d : 0.0;
         }
       }
+      tsum[s] = w;
     }
-    if (sidx < ns) tsum[sidx] = w;
+    const bool ok0 = !wave_reduce((int)over, OpOr());
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    // prefix sums over the sub-chunks in place (tsum[s] = mass through s),
+    // 64 at a time with a carry; each lane rewrites only its own entries
+    double carry = 0.0;
+    for (int s0 = 0; s0 < ns; s0 += 64) {
+      const double w = s0 + l < ns ? tsum[s0 + l] : 0.0;
+      const double incl = carry + wave_scan_dpp(w);
+      if (s0 + l < ns) tsum[s0 + l] = incl;
+      carry = lane_read(incl, 63);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    const double W = carry;
+    int state = 0, tok = -1;
+    if (W != W || St != St || Sq != Sq) {
+      state = 2;                                      // NaN probabilities: numpy raises
+    } else if (ok0 && W > err * St) {
+      // the sub-chunk holding u * W, and u's distance to its edges
+      int found = INT_MAX;
+      double gap = 1.0;
+      for (int s = l; s < ns; s += 64) {
+        const double lo = s > 0 ? tsum[s - 1] / W : 0.0, hi = tsum[s] / W;
+        if (lo <= u && u < hi) {
+          found = s;
+          gap = fmin(s > 0 ? u - lo : 1.0, s < ns - 1 ? hi - u : 1.0);
+        }
+      }
+      found = wave_reduce(found, OpMin());
+      gap = wave_reduce(gap, OpMin());
+      if (found != INT_MAX && gap > err) {
+        // the sub-chunk's elements in id order, eight consecutive per lane
+        const double before = found > 0 ? tsum[found - 1] : 0.0;
+        const int e0 = found * SUB + l * 8;
+        double w8[8];
+        double run = 0.0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int e = e0 + j;
+          double d = 0.0;
+          if (e < A.V)
+            d = exp64_neg(div32(tr[e], C.invT) - C.zmt, tab) -
+                lam * exp64_neg(div32(dr[e], C.invT) - C.zmq, tab);
+          run += d > 0.0 ? d : 0.0;
+          w8[j] = run;                                // inclusive prefix within the lane
+        }
+        const double incl = wave_scan_dpp(run);
+        const double lane0 = before + (incl - run);   // prefix before this lane
+        int hit = INT_MAX;
+        double margin = 1.0;
+#pragma unroll
+        for (int j = 7; j >= 0; --j) {
+          const int e = e0 + j;
+          if (e >= A.V) continue;
+          const double lo = (lane0 + (j > 0 ? w8[j - 1] : 0.0)) / W;
+          const double hi = (lane0 + w8[j]) / W;
+          if (lo <= u && u < hi) { hit = e; margin = fmin(u - lo, hi - u); }
+        }
+        hit = wave_reduce(hit, OpMin());
+        margin = wave_reduce(margin, OpMin());
+        if (hit != INT_MAX && margin > err) { state = 1; tok = hit; }
+      }
+    }
+    if (l == 0) {
+      s_state[0] = state;
+      s_state[1] = tok;
+      s_lam[0] = St; s_lam[1] = Sq;
+    }
   }
   __syncthreads();
-  const int nover = s_nover;
-  bool ok = nover <= 64;
-  for (int o = 0; o < nover && o < 64; ++o) {         // lists that overflowed: direct sums
-    const int sidx = s_over[o];
-    const int e = sidx * SUB + t;
-    double d = 0.0;
-    if (t < SUB && e < A.V)
-      d = exp64_neg(div32(tr[e], C.invT) - C.zmt, tab) -
-          lam * exp64_neg(div32(dr[e], C.invT) - C.zmq, tab);
-    d = block_sum(d > 0.0 ? d : 0.0, red_d);
-    if (t == 0) tsum[sidx] = d;
-    __syncthreads();
-  }
-  block_scan(tsum, ns, red_d);                        // inclusive prefix over sub-chunks
-  const double W = tsum[ns - 1];
-  if (W != W || St != St || Sq != Sq) {              // NaN probabilities: numpy raises
+  const int state = s_state[0];
+  int tok = s_state[1], flag = 0;
+  if (state == 2) {
     if (t == 0) {
       A.next_tok[b] = -1;
       A.used[b] = r + 1;
@@ -612,54 +665,9 @@ __global__ __launch_bounds__(WG) void verify_draw(VerifyArgs A) {
     }
     return;
   }
-  const double err = 1e-12;                           // relative rounding of the sums
-  ok = ok && W > err * St;
-  int tok = -1, flag = 0;
-  if (ok) {
-    // the sub-chunk holding u * W, and u's distance to its edges
-    int found = INT_MAX;
-    double gap = 1.0;
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      const int sidx = 2 * t + k;
-      if (sidx >= ns) continue;
-      const double lo = sidx > 0 ? tsum[sidx - 1] / W : 0.0, hi = tsum[sidx] / W;
-      if (lo <= u && u < hi) {
-        found = sidx;
-        gap = fmin(sidx > 0 ? u - lo : 1.0, sidx < ns - 1 ? hi - u : 1.0);
-      }
-    }
-    found = block_min(found, red_i, INT_MAX);
-    gap = block_min(gap, red_d, 1.0);
-    if (found == INT_MAX || gap <= err) ok = false;
-    if (ok) {
-      const double before = found > 0 ? tsum[found - 1] : 0.0;
-      __syncthreads();                                // tsum is reused below
-      const int e = found * SUB + t;
-      double w = 0.0;
-      if (t < SUB && e < A.V) {
-        const double d = exp64_neg(div32(tr[e], C.invT) - C.zmt, tab) -
-                         lam * exp64_neg(div32(dr[e], C.invT) - C.zmq, tab);
-        w = d > 0.0 ? d : 0.0;
-      }
-      if (t < SUB) tsum[t] = w;
-      __syncthreads();
-      block_scan(tsum, SUB, red_d);
-      int hit = INT_MAX;
-      double margin = 1.0;
-      if (t < SUB && e < A.V) {
-        const double lo = (before + (t > 0 ? tsum[t - 1] : 0.0)) / W;
-        const double hi = (before + tsum[t]) / W;
-        if (lo <= u && u < hi) { hit = e; margin = fmin(u - lo, hi - u); }
-      }
-      hit = block_min(hit, red_i, INT_MAX);
-      margin = block_min(margin, red_d, 1.0);
-      if (hit == INT_MAX || margin <= err) ok = false;
-      else tok = hit;
-    }
-  }
-  if (!ok) {                                          // exact fp64 redo over the row pair
-    __syncthreads();
+  if (state == 0) {                                   // exact fp64 redo over the row pair
+    C.invSt = 1.0 / s_lam[0];
+    C.invSq = 1.0 / s_lam[1];
     tok = exact_residual_draw(tr, dr, A.V, C, u, red_d, red_i, tsum);
     flag = CX_ROW_FLAG_EXACT;
     if (tok < 0) {                                    // R <= 0: argmax(row), no draw
