@@ -314,10 +314,28 @@ __device__ __forceinline__ double wave_incl_scan(double v) {
   return v;
 }
 
-// Sort n <= 2 * WG records held in LDS (k, i, a) into rec_before order.
-// Thread t owns elements t and t + WG.  Strides below 64 exchange through
-// cross-lane shuffles, larger strides through LDS.
+// Compare-exchange of a thread's own elements j and j ^ JS (elements
+// t + j * WG; stride JS * WG), with compile-time register indices.
+template <int JS, int R>
+__device__ __forceinline__ void own_stage(Rec (&r)[R], const bool (&have)[R], int t, int size) {
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    if ((j ^ JS) > j && (j ^ JS) < R && have[j ^ JS]) {
+      Rec lo = bitonic_pick(r[j], r[j ^ JS], t + j * WG, JS * WG, size);
+      Rec hi = bitonic_pick(r[j ^ JS], r[j], t + (j ^ JS) * WG, JS * WG, size);
+      r[j] = lo;
+      r[j ^ JS] = hi;
+    }
+  }
+}
+
+// Sort n <= R * WG records held in LDS (k, i, a) into rec_before order.
+// Thread t owns elements t + j * WG, j < R.  Strides of WG and more pair a
+// thread's own elements, strides from 64 to WG / 2 exchange through LDS,
+// smaller strides through cross-lane shuffles.
+template <int R = 2>
 __device__ inline void block_sort(uint64_t* k, int32_t* i, int32_t* a, int n) {
+  static_assert(R == 2 || R == 4, "R");
   int np = 2;
   while (np < n) np <<= 1;
   const int t = threadIdx.x;
@@ -340,54 +358,65 @@ __device__ inline void block_sort(uint64_t* k, int32_t* i, int32_t* a, int n) {
     __syncthreads();
     return;
   }
-  const bool two = np > WG;
-  Rec r0, r1;
-  r0.key = t < np ? k[t] : 0; r0.idx = t < np ? i[t] : INT_MAX; r0.aux = t < np ? a[t] : -1;
-  if (two) { r1.key = k[t + WG]; r1.idx = i[t + WG]; r1.aux = a[t + WG]; }
+  // np >= 128 here, so have[j] is uniform across each wave
+  Rec r[R];
+  bool have[R];
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    const int e = t + j * WG;
+    have[j] = e < np;
+    r[j].key = have[j] ? k[e] : 0;
+    r[j].idx = have[j] ? i[e] : INT_MAX;
+    r[j].aux = have[j] ? a[e] : -1;
+  }
   __syncthreads();
   for (int size = 2; size <= np; size <<= 1) {
     for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      if (stride >= WG) {                       // partner is the thread's other element
-        Rec lo = bitonic_pick(r0, r1, t, stride, size);
-        Rec hi = bitonic_pick(r1, r0, t + WG, stride, size);
-        r0 = lo; r1 = hi;
+      if (stride >= WG) {                       // partner is another of the thread's elements
+        if (stride == WG) own_stage<1, R>(r, have, t, size);
+        else if constexpr (R >= 4) own_stage<2, R>(r, have, t, size);
       } else if (stride >= 64) {                // partner in another wave: via LDS
-        if (t < np) { k[t] = r0.key; i[t] = r0.idx; a[t] = r0.aux; }
-        if (two) { k[t + WG] = r1.key; i[t + WG] = r1.idx; a[t + WG] = r1.aux; }
+#pragma unroll
+        for (int j = 0; j < R; ++j)
+          if (have[j]) { const int e = t + j * WG; k[e] = r[j].key; i[e] = r[j].idx; a[e] = r[j].aux; }
         __syncthreads();
-        if (t < np) {
-          int q = t ^ stride;
-          Rec p; p.key = k[q]; p.idx = i[q]; p.aux = a[q];
-          r0 = bitonic_pick(r0, p, t, stride, size);
-        }
-        if (two) {
-          int q = (t + WG) ^ stride;
-          Rec p; p.key = k[q]; p.idx = i[q]; p.aux = a[q];
-          r1 = bitonic_pick(r1, p, t + WG, stride, size);
-        }
+#pragma unroll
+        for (int j = 0; j < R; ++j)
+          if (have[j]) {
+            const int q = (t + j * WG) ^ stride;
+            Rec p; p.key = k[q]; p.idx = i[q]; p.aux = a[q];
+            r[j] = bitonic_pick(r[j], p, t + j * WG, stride, size);
+          }
         __syncthreads();
       } else {                                  // same wave: shuffles
-        Rec p0 = shfl_xor_rec(r0, stride);
-        r0 = bitonic_pick(r0, p0, t, stride, size);
-        if (two) {
-          Rec p1 = shfl_xor_rec(r1, stride);
-          r1 = bitonic_pick(r1, p1, t + WG, stride, size);
-        }
+#pragma unroll
+        for (int j = 0; j < R; ++j)
+          if (have[j]) {
+            Rec p = shfl_xor_rec(r[j], stride);
+            r[j] = bitonic_pick(r[j], p, t + j * WG, stride, size);
+          }
       }
     }
   }
-  if (t < np) { k[t] = r0.key; i[t] = r0.idx; a[t] = r0.aux; }
-  if (two) { k[t + WG] = r1.key; i[t + WG] = r1.idx; a[t + WG] = r1.aux; }
+#pragma unroll
+  for (int j = 0; j < R; ++j)
+    if (have[j]) { const int e = t + j * WG; k[e] = r[j].key; i[e] = r[j].idx; a[e] = r[j].aux; }
   __syncthreads();
 }
 
-// Inclusive prefix sum of v[0..n), n <= 2 * WG, in place (fp64).  Thread t
-// owns elements 2t and 2t+1.
+// Inclusive prefix sum of v[0..n), n <= R * WG, in place (fp64).  Thread t
+// owns elements R t .. R t + R - 1.
+template <int R = 2>
 __device__ inline void block_scan(double* v, int n, double* scratch) {
+  static_assert(R == 2 || R == 4, "R");
   const int t = threadIdx.x;
-  double a = 2 * t < n ? v[2 * t] : 0.0;
-  double b = 2 * t + 1 < n ? v[2 * t + 1] : 0.0;
-  double s = a + b;
+  double x[R];
+  double s = 0.0;
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    x[j] = R * t + j < n ? v[R * t + j] : 0.0;
+    s += x[j];
+  }
   double inc = s;                                // inclusive scan across the wave
   for (int o = 1; o < 64; o <<= 1) {
     double w = __shfl_up(inc, o);
@@ -397,17 +426,20 @@ __device__ inline void block_scan(double* v, int n, double* scratch) {
   __syncthreads();
   if (t < 64) {
     double w = t < NWAVE ? scratch[t] : 0.0;
-    double x = w;
+    double y = w;
     for (int o = 1; o < 64; o <<= 1) {
-      double y = __shfl_up(x, o);
-      if (t >= o) x += y;
+      double z = __shfl_up(y, o);
+      if (t >= o) y += z;
     }
-    if (t < NWAVE) scratch[NWAVE + t] = x - w;   // exclusive wave offsets
+    if (t < NWAVE) scratch[NWAVE + t] = y - w;   // exclusive wave offsets
   }
   __syncthreads();
-  double base = scratch[NWAVE + wave_id()] + (inc - s);
-  if (2 * t < n) v[2 * t] = base + a;
-  if (2 * t + 1 < n) v[2 * t + 1] = base + a + b;
+  double run = scratch[NWAVE + wave_id()] + (inc - s);
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    run += x[j];
+    if (R * t + j < n) v[R * t + j] = run;
+  }
   __syncthreads();
 }
 

@@ -66,10 +66,22 @@ __device__ inline uint64_t kth_candidate_key(const SampleArgs& A, int row, uint6
   return prefix;
 }
 
-// Returns false, with nothing written, when the row needs the exact
-// multi-pass path.
-__device__ inline bool finish_row_fast(const SampleArgs& A, int row, const cx_row_params& P,
-                                       unsigned char* dyn, double* red_d, int* red_i) {
+// Outcomes of finish_row_fast.
+constexpr int FIN_PENDING = 0;   // the exact multi-pass path must take the row
+constexpr int FIN_DONE = 1;      // decided and written
+constexpr int FIN_REFINE = 2;    // region complete, but a top-p cut lies within the
+                                 // normaliser's error bound: decide again with an
+                                 // exact fp64 normaliser
+
+// Finish a row from its region (at most CAP entries, CAP / WG per thread).
+// S_exact > 0 is the exact fp64 normaliser sum exp((x - M) / T) over the
+// row, replacing the slices' streamed sums; the top-p cut is then taken as
+// it falls.  Nothing is written unless the outcome is FIN_DONE.
+template <int CAP>
+__device__ inline int finish_row_fast(const SampleArgs& A, int row, const cx_row_params& P,
+                                      unsigned char* dyn, double* red_d, int* red_i,
+                                      double S_exact = 0.0) {
+  constexpr int R = CAP / WG;
   __shared__ int f_n;
   __shared__ int f_j;
   const int t = threadIdx.x;
@@ -80,7 +92,7 @@ __device__ inline bool finish_row_fast(const SampleArgs& A, int row, const cx_ro
 
   if (flags & SF_UNSUPPORTED) {
     write_row_result(A, row, CX_ROW_UNSUPPORTED, -1);
-    return true;
+    return FIN_DONE;
   }
   if (P.temperature == 0.0) {                      // sampler.py:114-115
     double bv = -__builtin_inf();
@@ -92,7 +104,7 @@ __device__ inline bool finish_row_fast(const SampleArgs& A, int row, const cx_ro
     int tok = ni != INT_MAX ? ni : (bi == INT_MAX ? 0 : bi);
     write_row_result(A, row, CX_ROW_GREEDY, tok);
     write_one_hot(A, row, tok);
-    return true;
+    return FIN_DONE;
   }
 
   const double invT = 1.0 / P.temperature;
@@ -110,21 +122,24 @@ __device__ inline bool finish_row_fast(const SampleArgs& A, int row, const cx_ro
     tau = max(tau, st[s].tau);
     tol = st[s].tol > tol ? st[s].tol : tol;
   }
+  const bool exact = S_exact > 0.0;
+  if (exact) S = S_exact;
   // Degenerate rows (NaN / +inf / all -inf), tie floods, typical-p and a
   // possible P**(1/T) underflow (ln V / T > 740) go to the multi-pass kernel.
-  if (mnan || !(S > 0.0) || !(S < __builtin_inf()) || (flags & (SF_OVERFLOW | SF_INEXACT)) ||
-      P.typical_p < 1.0 || A.logV * invT > 740.0) {
-    return false;
+  if (mnan || !(S > 0.0) || !(S < __builtin_inf()) ||
+      (flags & (SF_OVERFLOW | (exact ? 0 : SF_INEXACT))) || P.typical_p < 1.0 ||
+      A.logV * invT > 740.0) {
+    return FIN_PENDING;
   }
   bool region_incomplete_after_shrink = false;
   const bool region_all_pre = tau <= 1u;
   const uint64_t thr64 = region_all_pre ? 0ull : d2key((double)key2f(tau));
 
   uint64_t* skey = (uint64_t*)dyn;
-  int32_t* sidx = (int32_t*)(dyn + SORT_CAP * 8);
-  int32_t* saux = sidx + SORT_CAP;
-  double* sv = (double*)(dyn + SORT_CAP * 16);
-  double* sc = sv + SORT_CAP;
+  int32_t* sidx = (int32_t*)(dyn + CAP * 8);
+  int32_t* saux = sidx + CAP;
+  double* sv = (double*)(dyn + CAP * 16);
+  double* sc = sv + CAP;
 
   if (t == 0) f_n = 0;
   __syncthreads();
@@ -135,18 +150,18 @@ __device__ inline bool finish_row_fast(const SampleArgs& A, int row, const cx_ro
       Cand c = cs[e];
       if (c.key >= thr64) {
         int pos = atomicAdd(&f_n, 1);
-        if (pos < SORT_CAP) { skey[pos] = c.key; sidx[pos] = c.idx; saux[pos] = 0; }
+        if (pos < CAP) { skey[pos] = c.key; sidx[pos] = c.idx; saux[pos] = 0; }
       }
     }
   }
   __syncthreads();
   int E = f_n;
-  if (E > SORT_CAP) {
-    // Shrink the region to the SORT_CAP largest candidates (strictly above the
-    // SORT_CAP-th key when ties would overflow): it still holds every element
-    // of the row above its new threshold.
+  if (E > CAP) {
+    // Shrink the region to the CAP largest candidates (strictly above the
+    // CAP-th key when ties would overflow): it still holds every element of
+    // the row above its new threshold.
     __shared__ uint64_t bc[2];
-    uint64_t kk = kth_candidate_key(A, row, thr64, SORT_CAP, (uint32_t*)sv, bc);
+    uint64_t kk = kth_candidate_key(A, row, thr64, CAP, (uint32_t*)sv, bc);
     uint64_t thr2 = kk + 1;
     if (t == 0) f_n = 0;
     __syncthreads();
@@ -157,7 +172,7 @@ __device__ inline bool finish_row_fast(const SampleArgs& A, int row, const cx_ro
         Cand c = cs[e];
         if (c.key >= thr2) {
           int pos = atomicAdd(&f_n, 1);
-          if (pos < SORT_CAP) { skey[pos] = c.key; sidx[pos] = c.idx; saux[pos] = 0; }
+          if (pos < CAP) { skey[pos] = c.key; sidx[pos] = c.idx; saux[pos] = 0; }
         }
       }
     }
@@ -165,8 +180,8 @@ __device__ inline bool finish_row_fast(const SampleArgs& A, int row, const cx_ro
     E = f_n;
     region_incomplete_after_shrink = true;
   }
-  if (E > SORT_CAP || E == 0) return false;
-  block_sort(skey, sidx, saux, E);
+  if (E > CAP || E == 0) return FIN_PENDING;
+  block_sort<R>(skey, sidx, saux, E);
 
   const bool region_all = region_all_pre && !region_incomplete_after_shrink;
   // ---- top-k: every value >= the k-th largest (ties kept)
@@ -183,7 +198,7 @@ __device__ inline bool finish_row_fast(const SampleArgs& A, int row, const cx_ro
       nk = f_j;
       complete = true;
     } else if (!region_all) {
-      return false;
+      return FIN_PENDING;
     }
   }
   // ---- probabilities of the kept prefix
@@ -193,7 +208,7 @@ __device__ inline bool finish_row_fast(const SampleArgs& A, int row, const cx_ro
   if (P.top_p < 1.0) {
     for (int j = t; j < nk; j += WG) sc[j] = sv[j];
     __syncthreads();
-    block_scan(sc, nk, red_d);
+    block_scan<R>(sc, nk, red_d);
     if (t == 0) f_j = nk;
     __syncthreads();
     for (int j = t; j < nk; j += WG)
@@ -207,10 +222,10 @@ __device__ inline bool finish_row_fast(const SampleArgs& A, int row, const cx_ro
       nk = m + 1;
       complete = true;
     } else {
-      if (!complete) return false;
+      if (!complete) return FIN_PENDING;
       near = fabs(sc[nk - 1] - P.top_p) <= tol * sc[nk - 1];
     }
-    if (near) return false;
+    if (near && !exact) return FIN_REFINE;
   }
   // ---- min-p relative to the top probability
   if (P.min_p > 0.0) {
@@ -221,9 +236,9 @@ __device__ inline bool finish_row_fast(const SampleArgs& A, int row, const cx_ro
       if (sv[j] < floor_p) atomicMin(&f_j, j);
     __syncthreads();
     if (f_j < nk) { nk = f_j; complete = true; }
-    else if (!complete) return false;
+    else if (!complete) return FIN_PENDING;
   }
-  if (!complete) return false;
+  if (!complete) return FIN_PENDING;
 
   // ---- normalise and draw in token-id order
   double z = 0.0;
@@ -231,10 +246,10 @@ __device__ inline bool finish_row_fast(const SampleArgs& A, int row, const cx_ro
   const double Z = block_sum(z, red_d);
   for (int j = t; j < nk; j += WG) { skey[j] = ~(uint64_t)(uint32_t)sidx[j]; saux[j] = j; }
   __syncthreads();
-  block_sort(skey, sidx, saux, nk);
+  block_sort<R>(skey, sidx, saux, nk);
   for (int j = t; j < nk; j += WG) sc[j] = sv[saux[j]] / Z;
   __syncthreads();
-  block_scan(sc, nk, red_d);
+  block_scan<R>(sc, nk, red_d);
   const double last = sc[nk - 1];
   const double u = A.u[row];
   if (t == 0) f_j = nk - 1;
@@ -249,15 +264,18 @@ __device__ inline bool finish_row_fast(const SampleArgs& A, int row, const cx_ro
     __syncthreads();
     for (int j = t; j < nk; j += WG) p[sidx[j]] = (float)(sv[saux[j]] / Z);
   }
-  write_row_result(A, row, CX_ROW_OK, tok);
-  return true;
+  write_row_result(A, row, exact ? (CX_ROW_OK | CX_ROW_FLAG_EXACT) : CX_ROW_OK, tok);
+  return FIN_DONE;
 }
 
 // Finish a row from its slices' statistics and regions; a row this cannot
-// decide is marked pending for the exact multi-pass kernel.
+// decide is marked for the exact-normaliser refinement or, failing that, for
+// the exact multi-pass kernel.
+template <int CAP>
 __device__ inline void finish_row(const SampleArgs& A, int row, const cx_row_params& P,
                                   unsigned char* dyn, double* red_d, int* red_i) {
-  if (!finish_row_fast(A, row, P, dyn, red_d, red_i)) write_row_result(A, row, ROW_PENDING, -1);
+  const int r = finish_row_fast<CAP>(A, row, P, dyn, red_d, red_i);
+  if (r != FIN_DONE) write_row_result(A, row, r == FIN_REFINE ? ROW_REFINE : ROW_PENDING, -1);
 }
 
 }  // namespace cx

@@ -8,7 +8,8 @@ namespace cx {
 
 constexpr int CAPW = 256;                 // per-wave candidate buffer (entries)
 constexpr int KW_MAX = 128;               // entries a wave keeps when it compacts
-constexpr int SORT_CAP = 2048;            // finisher sort capacity (2 per thread)
+constexpr int SORT_CAP = 2048;            // in-kernel finisher sort capacity (2 per thread)
+constexpr int FIN_CAP = 4096;             // finish_kernel / refinement sort capacity (4 per thread)
 constexpr int WIN_MAX = 4095;             // longest penalty window held in LDS
 constexpr int CAPS = 16 * CAPW + 4096;    // candidates per (row, slice) in the workspace
 constexpr int LEAN_CAP = 256;             // region size the one-wave finisher sorts
@@ -23,9 +24,13 @@ constexpr int SF_UNSUPPORTED = 2;         // window longer than WIN_MAX
 constexpr int SF_INEXACT = 4;             // the slice's normaliser has no usable error bound
 
 
-// Internal row_status value: the fused path could not decide the row and
-// the exact multi-pass kernel must finish it.  Never returned to the caller.
+// Internal row_status values, never returned to the caller: the fused path
+// could not decide the row and the exact multi-pass kernel must finish it
+// (PENDING), or the row's region is complete and only a top-p cut within the
+// streamed normaliser's error bound is open, so the exact kernel recomputes
+// the normaliser in fp64 and finishes the region again (REFINE).
 constexpr int ROW_PENDING = 0x40000000;
+constexpr int ROW_REFINE = 0x40000001;
 
 struct SplitStats {       // one per (row, slice), 64 bytes
   double m;               // max of the slice's penalised values (stochastic rows)
@@ -59,7 +64,7 @@ struct SampleArgs {
   int32_t* out_id;
   int32_t* row_status;
   float* out_probs;
-  int32_t* counters;      // [B], zero between calls
+  int32_t* counters;      // [B], zero between calls (unused by the kernels)
   SplitStats* stats;      // [B * nsplit]
   Cand* cands;            // [B * nsplit * CAPS]
   int32_t nsplit, split_len;

@@ -687,9 +687,14 @@ __device__ __forceinline__ void lean_ranks(const CX_LDS uint64_t* gk, const CX_L
 // exp2(x c - Rb) / S within tol (relative) of the exact ones.  Returns false
 // when the row needs the exact path (near a top-p boundary, or more than
 // 64 entries tied into the top-k).
-__device__ inline bool lean_decide(const cx_row_params& P, const CX_LDS uint64_t* gk,
-                                   const CX_LDS int32_t* gi, int nlist, double kc, double Rb,
-                                   double S, double tol, CX_LDS LeanLds* L, double u, int& tok) {
+// Outcomes of lean_decide.
+constexpr int LEAN_PENDING = 0;  // the exact multi-pass path must take the row
+constexpr int LEAN_DONE = 1;
+constexpr int LEAN_NEAR = 2;     // a top-p cut within the normaliser's error bound
+
+__device__ inline int lean_decide(const cx_row_params& P, const CX_LDS uint64_t* gk,
+                                  const CX_LDS int32_t* gi, int nlist, double kc, double Rb,
+                                  double S, double tol, CX_LDS LeanLds* L, double u, int& tok) {
   const int l = lane_id();
   // the top 65 entries in value order, and every id at its id rank
   for (int e = l; e < nlist; e += 64) {
@@ -710,7 +715,7 @@ __device__ inline bool lean_decide(const cx_row_params& P, const CX_LDS uint64_t
   if (P.top_k < nlist) {
     const uint64_t kth = lane_read(key, P.top_k - 1);
     n = __popcll(ballot(l < E && key >= kth));
-    if (n == 64 && nlist > 64 && L->sk[64] == kth) return false;
+    if (n == 64 && nlist > 64 && L->sk[64] == kth) return LEAN_PENDING;
   }
   // (2) probabilities of the kept prefix; top-p on the unrenormalised vector
   const double Pj = l < n ? exp2(key2d(key) * kc - Rb) / S : 0.0;
@@ -728,7 +733,7 @@ __device__ inline bool lean_decide(const cx_row_params& P, const CX_LDS uint64_t
       const double cl = lane_read(cum, n - 1);
       near = fabs(cl - P.top_p) <= tol * cl;
     }
-    if (near) return false;                            // exact fp64 normaliser needed
+    if (near) return LEAN_NEAR;                        // exact fp64 normaliser needed
   }
   if (P.min_p > 0.0) {                                 // sampler.py:91-93
     const double floor_p = P.min_p * lane_read(Pj, 0);
@@ -763,7 +768,7 @@ __device__ inline bool lean_decide(const cx_row_params& P, const CX_LDS uint64_t
     if (4 * l + i < nlist && (base + f[i]) / last > u) first = 4 * l + i;
   const uint64_t b = ballot(first != INT_MAX);
   tok = b ? L->oid[lane_read(first, __builtin_ctzll(b))] : wave_reduce(l < n ? idx : -1, OpMax());
-  return true;
+  return LEAN_DONE;
 }
 
 // ------------------------------------------------------------ penalty corrections
@@ -1023,8 +1028,9 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   wb.tauf = -__builtin_inff();
   wb.overflow = false;
   // Entries a wave keeps: k for top-k rows; otherwise an equal share of the
-  // finisher's sort capacity, so the merged region fits in LDS.
-  const int share = max(8, min(KW_MAX, SORT_CAP / (NWAVE * A.nsplit)));
+  // finisher's sort capacity (in this kernel for one slice per row, in
+  // finish_kernel for several), so the merged region fits in LDS.
+  const int share = max(8, min(KW_MAX, (single ? SORT_CAP : FIN_CAP) / (NWAVE * A.nsplit)));
   wb.kw = P.top_k > 0 ? min(P.top_k, KW_MAX) : share;
   // elements the shared threshold must leave: k of a top-k row, or 1024
   // region entries of a top-p row
@@ -1158,10 +1164,31 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
     __syncthreads();
     if (wave_id() != 0) return;
     int tok = -1;
-    ok = ok && lean_decide(P, lgk, lgi, nlist, kc, Rb, Ss, tol, L, u_row, tok);
+    const int dr = ok ? lean_decide(P, lgk, lgi, nlist, kc, Rb, Ss, tol, L, u_row, tok)
+                      : LEAN_PENDING;
+    if (dr == LEAN_NEAR) {
+      // the list as the row's region (every element at or above the largest
+      // wave threshold), for the exact-normaliser refinement
+      uint64_t kmax = 0ull;
+      for (int e = lane_id(); e < nlist; e += 64) {
+        const uint64_t k = lgk[e];
+        mycand[e].key = k;
+        mycand[e].idx = lgi[e];
+        kmax = k > kmax ? k : kmax;
+      }
+      kmax = wave_reduce(kmax, OpMax());
+      const uint32_t tmax = row0_reduce(w_tau[lw], OpMax());
+      if (lane_id() == 0) {
+        my->m = key2d(kmax);
+        my->s = Ss;
+        my->tol = tol;
+        my->best_v = 0; my->best_i = INT_MAX; my->nan_i = INT_MAX;
+        my->tau = tmax; my->ncand = nlist; my->flags = 0;
+      }
+    }
     if (lane_id() == 0) {
-      A.out_id[row] = ok ? tok : -1;
-      A.row_status[row] = ok ? CX_ROW_OK : ROW_PENDING;
+      A.out_id[row] = dr == LEAN_DONE ? tok : -1;
+      A.row_status[row] = dr == LEAN_DONE ? CX_ROW_OK : (dr == LEAN_NEAR ? ROW_REFINE : ROW_PENDING);
     }
     return;
   }
@@ -1244,7 +1271,7 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   // results visible across XCDs without per-workgroup cache writebacks).
   if (!single) return;
   __syncthreads();
-  finish_row(A, row, P, dyn, red_d, red_i);
+  finish_row<SORT_CAP>(A, row, P, dyn, red_d, red_i);
 }
 
 // Finisher for rows computed in several slices: one workgroup per row.
@@ -1254,7 +1281,7 @@ __global__ __launch_bounds__(WG) void finish_kernel(SampleArgs A) {
   __shared__ int red_i[2 * NWAVE + 4];
   const int row = blockIdx.x;
   const cx_row_params P = A.prm[row];
-  finish_row(A, row, P, dyn, red_d, red_i);
+  finish_row<FIN_CAP>(A, row, P, dyn, red_d, red_i);
 }
 
 template __global__ void sample_kernel<false>(SampleArgs);

@@ -1,27 +1,61 @@
 // cx_slow.hip -- kernels built on the exact multi-pass row path
 // (cx_slow.hpp):
 //   slow_kernel       the rows the fused sampler left pending (or, for fp64
-//                     logits, every row).  One workgroup per row; a
-//                     workgroup whose row is decided reads its status word
-//                     and exits.
+//                     logits, every row), and the rows it left for
+//                     refinement: their normaliser recomputed exactly in
+//                     fp64, then the region finished again.  One workgroup
+//                     per row; a workgroup whose row is decided reads its
+//                     status word and exits.
 //   penalties_kernel  Sampler.apply_penalties, grid (rows, chunks of PEN_CHUNK)
 //   truncate_kernel   Sampler._truncate, one workgroup per row
 #include "cx_slow.hpp"
+#include "cx_finish.hpp"
 #include "cx_timing.hpp"
 
 namespace cx {
 
 constexpr int PEN_CHUNK = 16384;     // elements per penalties_kernel workgroup
 
+// A row whose region is complete and whose only open question is a top-p
+// cut within the streamed normaliser's error bound: the exact fp64
+// normaliser over the row, then the region finished with it.  Returns false,
+// with nothing written, if the row still needs the multi-pass path.
+__device__ inline bool refine_row(const SampleArgs& A, int row, unsigned char* dyn, double* red_d,
+                                  int* red_i) {
+  const cx_row_params P = A.prm[row];
+  SlowRow R;
+  const int wlen = slow_setup(A, row, P, dyn, R);
+  if (wlen > WIN_MAX || !(P.temperature > 0.0)) return false;
+  // the row's maximum penalised value, as the finisher takes it
+  double M = -__builtin_inf();
+  for (int s = 0; s < A.nsplit; ++s) {
+    const double m = A.stats[(size_t)row * A.nsplit + s].m;
+    M = m > M ? m : M;
+  }
+  if (!(M > -__builtin_inf()) || !(M < __builtin_inf())) return false;
+  const double S = exact_norm(R, M, 1.0 / P.temperature, red_d);
+  __syncthreads();                       // the penalty tables in dyn are dead from here
+  if (!(S > 0.0) || !(S < __builtin_inf())) return false;
+  return finish_row_fast<FIN_CAP>(A, row, P, dyn, red_d, red_i, S) == FIN_DONE;
+}
+
 __global__ __launch_bounds__(WG) void slow_kernel(SampleArgs A) {
   extern __shared__ __align__(16) unsigned char dyn[];
   __shared__ double red_d[2 * NWAVE + 4];
   __shared__ int red_i[2 * NWAVE + 4];
-  __shared__ int s_pending;
+  __shared__ int s_state;
   const int row = blockIdx.x;
-  if (threadIdx.x == 0) s_pending = A.all_slow || A.row_status[row] == ROW_PENDING;
+  if (threadIdx.x == 0) {
+    const int st = A.row_status[row];
+    s_state = A.all_slow || st == ROW_PENDING ? 1 : (st == ROW_REFINE ? 2 : 0);
+  }
   __syncthreads();
-  if (s_pending) slow_row(A, row, dyn, red_d, red_i);
+  const int state = s_state;
+  if (state == 2 && refine_row(A, row, dyn, red_d, red_i)) return;
+  if (state != 0) {
+    __syncthreads();
+    slow_row(A, row, dyn, red_d, red_i);
+  }
 }
 
 __global__ __launch_bounds__(WG) void penalties_kernel(SampleArgs A) {
@@ -52,8 +86,10 @@ static int set_lds(K kernel, int bytes, int& attr) {
 
 int launch_slow(const SampleArgs& A, hipStream_t s) {
   static int attr = 0;
-  if (int e = set_lds(slow_kernel, A.slow_lds_bytes, attr)) return e;
-  timed_launch(CX_KERNEL_SAMPLE_SLOW, slow_kernel, dim3(A.B), dim3(WG), A.slow_lds_bytes, s, A);
+  // the multi-pass layout, or a refined row's finisher region
+  const int bytes = max(A.slow_lds_bytes, FIN_CAP * 32);
+  if (int e = set_lds(slow_kernel, bytes, attr)) return e;
+  timed_launch(CX_KERNEL_SAMPLE_SLOW, slow_kernel, dim3(A.B), dim3(WG), bytes, s, A);
   return (int)hipGetLastError();
 }
 

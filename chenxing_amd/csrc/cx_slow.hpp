@@ -2,9 +2,10 @@
 //
 // Finishes the rows the fused kernel cannot decide: degenerate rows (NaN,
 // +inf, all -inf, P**(1/T) underflow), nuclei or top-k sets deeper than the
-// fused kernel's region, tie floods, top-p decisions within the fused
-// normaliser's error bound, and typical-p.  One workgroup per row; every
-// quantity is fp64 and every selection is exact:
+// fused kernel's region, tie floods, and typical-p.  (A top-p cut within the
+// fused normaliser's error bound over a complete region is refined instead:
+// exact_norm below, then the region finisher again.)  One workgroup per row;
+// every quantity is fp64 and every selection is exact:
 //
 //   pass A   max / first argmax / first NaN / min of the penalised row
 //   pass B   S = sum exp((x - M) / T)  (and the T = 1 sum for the underflow test)
@@ -53,9 +54,9 @@ __device__ __forceinline__ double raw_at(const SlowRow& R, int i) {
                 : (double)((const float*)R.rowp)[i];
 }
 
-// Penalised fp64 value of element i (sampler.py:65-72 + presence/frequency).
-__device__ inline double value_at(const SlowRow& R, int i) {
-  double x = raw_at(R, i);
+// Penalised fp64 value of element i whose raw value is x (sampler.py:65-72
+// + presence/frequency).
+__device__ inline double penalise_at(const SlowRow& R, int i, double x) {
   if (R.pen && ((R.bitmap[(i >> 5) & (R.nbw - 1)] >> (i & 31)) & 1u)) {
     const uint32_t mask = (1u << R.ns_log2) - 1;
     uint32_t s = s_hash_slot(i, R.ns_log2);
@@ -74,6 +75,34 @@ __device__ inline double value_at(const SlowRow& R, int i) {
     }
   }
   return x;
+}
+
+__device__ __forceinline__ double value_at(const SlowRow& R, int i) {
+  return penalise_at(R, i, raw_at(R, i));
+}
+
+// sum over the row of exp((x - M) / T), x the penalised fp64 values (the
+// reference's normaliser, sampler.py:119-123), in fp64.  Every thread keeps
+// EXN independent loads in flight per step; the result is the same on every
+// thread.
+__device__ inline double exact_norm(const SlowRow& R, double M, double invT, double* red_d) {
+  constexpr int EXN = 8;
+  const int t = threadIdx.x;
+  double s = 0.0;
+  for (int base = 0; base < R.V; base += EXN * WG) {
+    double x[EXN];
+#pragma unroll
+    for (int j = 0; j < EXN; ++j) {
+      const int i = base + j * WG + t;
+      x[j] = i < R.V ? raw_at(R, i) : 0.0;
+    }
+#pragma unroll
+    for (int j = 0; j < EXN; ++j) {
+      const int i = base + j * WG + t;
+      if (i < R.V) s += exp((penalise_at(R, i, x[j]) - M) * invT);
+    }
+  }
+  return block_sum(s, red_d);
 }
 
 __device__ __forceinline__ double mass_of(const SlowRow& R, double v) {

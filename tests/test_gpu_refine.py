@@ -1,0 +1,92 @@
+"""Rows whose top-p cut lies within the fused normaliser's error bound: the
+exact kernel recomputes the normaliser in fp64 and finishes the row's region
+again (CX_ROW_FLAG_EXACT) instead of running the multi-pass path
+(CX_ROW_FLAG_SLOW).  Each constructed row puts top_p 1e-9 (relative) from
+one of the oracle's cumulative sums, so only an exact normaliser decides it;
+the device's token must equal the oracle's exactly."""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+
+from chenxing_amd import workloads as W
+from chenxing_amd._lib import FLAG_EXACT, FLAG_SLOW, sample_host
+from chenxing_amd.params import RowParams
+from oracle import sampler_ref as R
+from parity import compare_rows, oracle_rows
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def _near_cut_rows(rng, x, hist, kw, m_lo, m_hi, rel=1e-9):
+    """Per row, top_p just below (even rows) or just above (odd rows) the
+    oracle's cumulative sum at a random rank m of the post-top-k vector."""
+    prms = []
+    for b in range(x.shape[0]):
+        base = RowParams(**kw)
+        h = None if hist is None else [int(t) for t in hist[b]]
+        P = R.tempered_probs(R.penalize(x[b], h, base), base.temperature)
+        if base.top_k > 0:
+            P = R.truncate(P, base, tie="stable")
+        run = np.cumsum(P[np.argsort(-P, kind="stable")])
+        m = int(rng.integers(m_lo, m_hi))
+        side = 1.0 if b % 2 else -1.0
+        prms.append(RowParams(**kw, top_p=float(run[m] * (1.0 + side * rel))))
+    return prms
+
+
+def _check_exact(x, prms, hist, u, want_probs, label):
+    B = x.shape[0]
+    hl = None if hist is None else np.full(B, hist.shape[1], np.int32)
+    _say(f"[gpu] refine {label} B={B} V={x.shape[1]} probs={want_probs}")
+    ids, st, probs = sample_host(x, prms, hist, hl, u, want_probs=want_probs)
+    orc = [R.sample_row(x[b], prms[b], None if hist is None else [int(t) for t in hist[b]],
+                        float(u[b]), tie="stable", keep_probs=want_probs) for b in range(B)]
+    t = compare_rows(ids, st, probs, orc, label)
+    assert not t.mismatches, t.mismatches[:5]
+    want = np.array([o.token for o in orc])
+    assert np.array_equal(ids, want), np.flatnonzero(ids != want)[:8]
+    assert not np.any(st & FLAG_SLOW), np.flatnonzero(st & FLAG_SLOW)[:8]
+    assert np.all(st & FLAG_EXACT), np.flatnonzero((st & FLAG_EXACT) == 0)[:8]
+
+
+@pytest.mark.parametrize("want_probs", [False, True])
+def test_near_cut_top_k_rows_with_penalties(want_probs):
+    """One slice per row (B = 256): without probabilities out the one-wave
+    top-k finish hands the row over, with them the block finisher does."""
+    rng = np.random.default_rng(21)
+    B, V, H = 256, 32000, 256
+    x = rng.normal(0, 2, (B, V)).astype(np.float32)
+    hist = W.zipf_history(rng, B, H, V).astype(np.int32)
+    kw = dict(temperature=0.8, top_k=40, repetition_penalty=1.1, presence_penalty=0.5,
+              frequency_penalty=0.3)
+    prms = _near_cut_rows(rng, x, hist, kw, 3, 30)
+    _check_exact(x, prms, hist, rng.random(B), want_probs, "top-k near cut")
+
+
+@pytest.mark.parametrize("want_probs", [False, True])
+def test_near_cut_nucleus_rows_in_slices(want_probs):
+    """Several slices per row (B = 8): finish_kernel hands the row over."""
+    rng = np.random.default_rng(22)
+    B, V = 8, 128256
+    x = rng.normal(0, 2, (B, V)).astype(np.float32)
+    prms = _near_cut_rows(rng, x, None, dict(temperature=1.0), 100, 1000)
+    _check_exact(x, prms, None, rng.random(B), want_probs, "nucleus near cut")
+
+
+def test_nucleus_config_avoids_multipass_path():
+    """B = 64 top-p 0.95 rows: every nucleus fits the sliced region and the
+    rows near the cut are refined, so no row takes the multi-pass path."""
+    w = W.nucleus()
+    _say(f"[gpu] refine {w.name} B={w.B} V={w.V}")
+    ids, st, probs = sample_host(w.logits, w.params, None, w.hist_len, w.u, want_probs=True)
+    t = compare_rows(ids, st, probs, oracle_rows(w), w.name)
+    assert not t.mismatches, t.mismatches[:5]
+    assert not np.any(st & FLAG_SLOW), np.flatnonzero(st & FLAG_SLOW)
