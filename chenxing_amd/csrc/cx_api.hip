@@ -139,15 +139,7 @@ static int sample_impl(const void* logits, int dtype, int64_t ld, int32_t B, int
   off += (size_t)16 * CAPW * 4;
   A.off_gather = (int)off;
   off += (size_t)LEAN_CAP * 12;
-  // finisher regions: key, id, aux, value and scan per entry; in this
-  // kernel for one slice per row, in finish_kernel for several
-  const size_t fin1 = (size_t)SORT_CAP * (8 + 4 + 4 + 8 + 8);
-  size_t fin = (size_t)FIN_CAP * (8 + 4 + 4 + 8 + 8);
-  const size_t so = (size_t)A.slow_lds_bytes;
-  if (so > fin) fin = so;
-  if (so > off) off = so;
-  A.fin_lds_bytes = (int)fin;
-  A.lds_bytes = (int)(A.nsplit > 1 ? off : (off > fin1 ? off : fin1));
+  A.lds_bytes = (int)off;
   if (A.lds_bytes > 150 * 1024) return fail(CX_EINVAL, "LDS layout too large (%d)", A.lds_bytes);
   hipStream_t s = (hipStream_t)stream;
   int e = 0;

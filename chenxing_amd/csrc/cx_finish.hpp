@@ -66,12 +66,244 @@ __device__ inline uint64_t kth_candidate_key(const SampleArgs& A, int row, uint6
   return prefix;
 }
 
+// ------------------------------------------------------------ bucketed cuts
+// The finisher's cuts (the k-th largest value, the top-p prefix, the draw in
+// token-id order) without sorting the region: entries go to NBK buckets that
+// are monotone in the order (linear in the value, or in the token id); the
+// buckets' weights are summed as fixed-point integers with LDS atomics
+// (exact, so independent of the order of the additions), scanned, and only
+// the bucket that holds the cut is gathered, sorted by one wave and scanned.
+constexpr int NBK = WG;            // buckets: one per thread in the scan
+constexpr int GBK = 64;            // a gathered bucket: one entry per lane
+constexpr double FX_MASS = 1152921504606846976.0;   // 2^60: masses sum to <= ~1
+
+// Inclusive prefix sum across the 64 lanes (integers).
+__device__ __forceinline__ unsigned long long wave_incl_scan_u64(unsigned long long v) {
+  for (int o = 1; o < 64; o <<= 1) {
+    const unsigned long long w = __shfl_up(v, o);
+    if (lane_id() >= o) v += w;
+  }
+  return v;
+}
+
+struct PrefixCut {
+  int found;        // the running weight reaches the target inside the entries
+  int overflow;     // the cut's bucket holds more than GBK entries
+  int bucket, pos, n;
+  double cum;       // running weight up to and including the cut entry
+  double prev;      // running weight before it
+  double total;     // weight of all eligible entries
+  uint64_t key;     // the cut entry's order key and token id
+  int32_t idx;
+};
+
+// The first eligible entry, in the order (bucket_of ascending, then key
+// descending, then id ascending), at which the running weight reaches
+// (>= target) or, if strict, passes (> target) the target; a relative
+// target is a fraction of the total.  Weights are scaled by `scale` into
+// integers (1 for counts).  On return `out` (shared) holds the cut and, with
+// `found`, ga[0 .. n) the region indices of the cut bucket's entries in
+// order.  All threads; uniform result.
+template <typename BucketOf, typename KeyOf, typename Weight, typename Elig>
+__device__ inline void prefix_cut(int E, const int32_t* sidx, BucketOf bucket_of, KeyOf key_of,
+                                  Weight weight, Elig elig, double scale, double target,
+                                  bool relative, bool strict, unsigned long long* bm,
+                                  uint64_t* gk, int32_t* gi, int32_t* ga, double* red_d,
+                                  int* red_i, PrefixCut& out) {
+  __shared__ int pc_n;
+  const int t = threadIdx.x;
+  unsigned long long* red_u = (unsigned long long*)red_d;
+  bm[t] = 0ull;
+  if (t == 0) pc_n = 0;
+  __syncthreads();
+  for (int j = t; j < E; j += WG)
+    if (elig(j)) atomicAdd(&bm[bucket_of(j)], (unsigned long long)(weight(j) * scale));
+  __syncthreads();
+  // exclusive scan of the buckets (thread t owns bucket t)
+  const unsigned long long mine = bm[t];
+  const unsigned long long inc = wave_incl_scan_u64(mine);
+  if (lane_id() == 63) red_u[wave_id()] = inc;
+  __syncthreads();
+  if (t < 64) {
+    const unsigned long long w = t < NWAVE ? red_u[t] : 0ull;
+    const unsigned long long x = wave_incl_scan_u64(w);
+    if (t < NWAVE) red_u[NWAVE + t] = x - w;
+    if (t == NWAVE - 1) red_u[2 * NWAVE] = x;
+  }
+  __syncthreads();
+  const unsigned long long base = red_u[NWAVE + wave_id()] + (inc - mine);
+  const double total = (double)red_u[2 * NWAVE] / scale;
+  const double tgt = relative ? target * total : target;
+  const double be = (double)(base + mine) / scale;
+  const bool hit = mine != 0ull && (strict ? be > tgt : be >= tgt);
+  const int bc = block_min(hit ? t : INT_MAX, red_i, INT_MAX);
+  if (bc == INT_MAX) {
+    if (t == 0) { out.found = 0; out.overflow = 0; out.total = total; }
+    __syncthreads();
+    return;
+  }
+  if (t == bc) red_u[2 * NWAVE + 1] = base;          // the weight before the cut bucket
+  // gather the cut bucket
+  for (int j = t; j < E; j += WG)
+    if (elig(j) && bucket_of(j) == bc) {
+      const int q = atomicAdd(&pc_n, 1);
+      if (q < GBK) { gk[q] = key_of(j); gi[q] = sidx[j]; ga[q] = j; }
+    }
+  __syncthreads();
+  const int n = pc_n;
+  if (n > GBK) {
+    if (t == 0) { out.found = 0; out.overflow = 1; out.total = total; }
+    __syncthreads();
+    return;
+  }
+  if (wave_id() == 0) {
+    const int l = lane_id();
+    Rec r[1];
+    r[0].key = l < n ? gk[l] : 0ull;
+    r[0].idx = l < n ? gi[l] : INT_MAX;
+    r[0].aux = l < n ? ga[l] : -1;
+    wave_sort<1>(r);
+    const double w = l < n ? weight(r[0].aux) : 0.0;
+    const double incl = wave_scan_dpp(w);
+    if (l < n) ga[l] = r[0].aux;
+    const unsigned long long bb = red_u[2 * NWAVE + 1];
+    const double based = (double)bb / scale;
+    const double cum = based + incl, prv = based + (incl - w);
+    const uint64_t hb = ballot(l < n && (strict ? cum > tgt : cum >= tgt));
+    const int pos = hb ? __builtin_ctzll(hb) : n - 1;
+    if (l == pos) {
+      out.found = 1; out.overflow = 0; out.bucket = bc; out.pos = pos; out.n = n;
+      out.cum = cum; out.prev = prv; out.total = total; out.key = r[0].key; out.idx = r[0].idx;
+    }
+  }
+  __syncthreads();
+}
+
 // Outcomes of finish_row_fast.
 constexpr int FIN_PENDING = 0;   // the exact multi-pass path must take the row
 constexpr int FIN_DONE = 1;      // decided and written
 constexpr int FIN_REFINE = 2;    // region complete, but a top-p cut lies within the
                                  // normaliser's error bound: decide again with an
                                  // exact fp64 normaliser
+
+constexpr int FIN_SORTED = 3;    // (finish_bucketed) a cut bucket overflowed: sort instead
+
+// The filters and the draw of finish_row_fast over the region held in LDS
+// (skey, sidx: E entries), with bucketed cuts.  kf, sv and sc are work
+// space (kf: kept flags, sv: the entries' probabilities, sc: buckets and the
+// gathered bucket).  Returns FIN_SORTED, with nothing written, when a cut's
+// bucket holds more than GBK entries (a flood of near-equal values).
+__device__ inline int finish_bucketed(const SampleArgs& A, int row, const cx_row_params& P,
+                                      const uint64_t* skey, const int32_t* sidx, int32_t* kf,
+                                      double* sv, double* sc, int E, bool region_all, double M,
+                                      double invT, double S, double tol, bool exact,
+                                      double* red_d, int* red_i) {
+  __shared__ PrefixCut pc;
+  const int t = threadIdx.x;
+  unsigned long long* bm = (unsigned long long*)sc;
+  uint64_t* gk = (uint64_t*)(sc + NBK);
+  int32_t* gi = (int32_t*)(gk + GBK);
+  int32_t* ga = gi + GBK;
+  uint64_t kmax = 0ull, kmin = ~0ull;
+  for (int j = t; j < E; j += WG) {
+    const uint64_t k = skey[j];
+    sv[j] = exp((key2d(k) - M) * invT) / S;
+    kf[j] = 1;
+    kmax = k > kmax ? k : kmax;
+    kmin = k < kmin ? k : kmin;
+  }
+  kmax = block_max<unsigned long long>(kmax, (unsigned long long*)red_d, 0ull);
+  kmin = block_min<unsigned long long>(kmin, (unsigned long long*)red_d, ~0ull);
+  // value buckets: linear in the value, bucket 0 holding the largest
+  const double vmax = key2d(kmax), vmin = key2d(kmin);
+  double vs = vmax > vmin ? (double)(NBK - 1) / (vmax - vmin) : 0.0;
+  if (!(vs < 1e300)) vs = 0.0;
+  // (vmax - v) * vs >= 0, or NaN for -inf values when vs == 0: the last bucket
+  auto vbucket = [&](int j) {
+    const double x = (vmax - key2d(skey[j])) * vs;
+    return x < (double)(NBK - 1) ? (int)x : NBK - 1;
+  };
+  auto vkey = [&](int j) { return skey[j]; };
+  // token-id buckets, ascending ids (key ~id orders descending keys as ascending ids)
+  auto ibucket = [&](int j) { return (int)(((long long)sidx[j] * NBK) / A.V); };
+  auto ikey = [&](int j) { return ~(uint64_t)(uint32_t)sidx[j]; };
+  auto one = [&](int) { return 1.0; };
+  auto mass = [&](int j) { return sv[j]; };
+  auto every = [&](int) { return true; };
+  auto kept = [&](int j) { return kf[j] != 0; };
+
+  bool complete = region_all;
+  // ---- top-k: every value >= the k-th largest (ties kept)
+  if (P.top_k > 0) {
+    if (P.top_k <= E) {
+      prefix_cut(E, sidx, vbucket, vkey, one, every, 1.0, (double)P.top_k, false, false, bm, gk,
+                 gi, ga, red_d, red_i, pc);
+      if (pc.overflow || !pc.found) return FIN_SORTED;
+      const uint64_t kth = pc.key;
+      for (int j = t; j < E; j += WG) kf[j] = skey[j] >= kth;
+      __syncthreads();
+      complete = true;
+    } else if (!region_all) {
+      return FIN_PENDING;
+    }
+  }
+  // ---- top-p on the unrenormalised vector: the shortest prefix in (value
+  // desc, id asc) order whose running mass reaches top_p
+  if (P.top_p < 1.0) {
+    prefix_cut(E, sidx, vbucket, vkey, mass, kept, FX_MASS, P.top_p, false, false, bm, gk, gi, ga,
+               red_d, red_i, pc);
+    if (pc.overflow) return FIN_SORTED;
+    bool near;
+    if (pc.found) {
+      const double cm = pc.cum, cp = pc.prev;
+      near = fabs(cm - P.top_p) <= tol * cm || (cp > 0.0 && fabs(cp - P.top_p) <= tol * cp);
+      const int bc = pc.bucket, pos = pc.pos;
+      for (int j = t; j < E; j += WG)
+        if (kf[j] && vbucket(j) >= bc) kf[j] = 0;
+      __syncthreads();
+      if (t <= pos) kf[ga[t]] = 1;       // the cut bucket's entries up to the cut
+      __syncthreads();
+      complete = true;
+    } else {
+      if (!complete) return FIN_PENDING;
+      near = fabs(pc.total - P.top_p) <= tol * pc.total;
+    }
+    if (near && !exact) return FIN_REFINE;
+  }
+  // ---- min-p relative to the top probability (the largest entry is kept)
+  if (P.min_p > 0.0) {
+    const double floor_p = P.min_p * (exp((vmax - M) * invT) / S);
+    int below = 0;
+    for (int j = t; j < E; j += WG)
+      if (kf[j] && sv[j] < floor_p) { kf[j] = 0; below = 1; }
+    below = block_max(below, red_i, 0);
+    if (below) complete = true;
+    else if (!complete) return FIN_PENDING;
+  }
+  if (!complete) return FIN_PENDING;
+
+  // ---- normalise and draw in token-id order: the first id whose running
+  // mass passes u times the kept total (Generator.choice)
+  double z = 0.0;
+  int lastk = -1;
+  for (int j = t; j < E; j += WG)
+    if (kf[j]) { z += sv[j]; lastk = max(lastk, sidx[j]); }
+  const double Z = block_sum(z, red_d);
+  prefix_cut(E, sidx, ibucket, ikey, mass, kept, FX_MASS, A.u[row], true, true, bm, gk, gi, ga,
+             red_d, red_i, pc);
+  if (pc.overflow) return FIN_SORTED;
+  // u beyond the last step by rounding: the last kept id
+  const int tok = pc.found ? pc.idx : block_max(lastk, red_i, -1);
+  if (A.out_probs) {
+    float* p = A.out_probs + (size_t)row * A.V;
+    for (int i = t; i < A.V; i += WG) p[i] = 0.0f;
+    __syncthreads();
+    for (int j = t; j < E; j += WG)
+      if (kf[j]) p[sidx[j]] = (float)(sv[j] / Z);
+  }
+  write_row_result(A, row, exact ? (CX_ROW_OK | CX_ROW_FLAG_EXACT) : CX_ROW_OK, tok);
+  return FIN_DONE;
+}
 
 // Finish a row from its region (at most CAP entries, CAP / WG per thread).
 // S_exact > 0 is the exact fp64 normaliser sum exp((x - M) / T) over the
@@ -181,9 +413,15 @@ __device__ inline int finish_row_fast(const SampleArgs& A, int row, const cx_row
     region_incomplete_after_shrink = true;
   }
   if (E > CAP || E == 0) return FIN_PENDING;
+  const bool region_all = region_all_pre && !region_incomplete_after_shrink;
+  {
+    const int rb = finish_bucketed(A, row, P, skey, sidx, saux, sv, sc, E, region_all, M, invT, S,
+                                   tol, exact, red_d, red_i);
+    if (rb != FIN_SORTED) return rb;
+  }
+  // a cut's bucket overflowed (near-equal values): sort the region instead
   block_sort<R>(skey, sidx, saux, E);
 
-  const bool region_all = region_all_pre && !region_incomplete_after_shrink;
   // ---- top-k: every value >= the k-th largest (ties kept)
   int nk = E;
   bool complete = region_all;
@@ -268,14 +506,5 @@ __device__ inline int finish_row_fast(const SampleArgs& A, int row, const cx_row
   return FIN_DONE;
 }
 
-// Finish a row from its slices' statistics and regions; a row this cannot
-// decide is marked for the exact-normaliser refinement or, failing that, for
-// the exact multi-pass kernel.
-template <int CAP>
-__device__ inline void finish_row(const SampleArgs& A, int row, const cx_row_params& P,
-                                  unsigned char* dyn, double* red_d, int* red_i) {
-  const int r = finish_row_fast<CAP>(A, row, P, dyn, red_d, red_i);
-  if (r != FIN_DONE) write_row_result(A, row, r == FIN_REFINE ? ROW_REFINE : ROW_PENDING, -1);
-}
 
 }  // namespace cx

@@ -8,8 +8,7 @@ namespace cx {
 
 constexpr int CAPW = 256;                 // per-wave candidate buffer (entries)
 constexpr int KW_MAX = 128;               // entries a wave keeps when it compacts
-constexpr int SORT_CAP = 2048;            // in-kernel finisher sort capacity (2 per thread)
-constexpr int FIN_CAP = 4096;             // finish_kernel / refinement sort capacity (4 per thread)
+constexpr int FIN_CAP = 4096;             // region finisher capacity (4 entries per thread)
 constexpr int WIN_MAX = 4095;             // longest penalty window held in LDS
 constexpr int CAPS = 16 * CAPW + 4096;    // candidates per (row, slice) in the workspace
 constexpr int LEAN_CAP = 256;             // region size the one-wave finisher sorts
@@ -24,13 +23,16 @@ constexpr int SF_UNSUPPORTED = 2;         // window longer than WIN_MAX
 constexpr int SF_INEXACT = 4;             // the slice's normaliser has no usable error bound
 
 
-// Internal row_status values, never returned to the caller: the fused path
-// could not decide the row and the exact multi-pass kernel must finish it
-// (PENDING), or the row's region is complete and only a top-p cut within the
-// streamed normaliser's error bound is open, so the exact kernel recomputes
-// the normaliser in fp64 and finishes the region again (REFINE).
+// Internal row_status values, never returned to the caller, for slow_kernel:
+// the fused path could not decide the row and the exact multi-pass path must
+// finish it (PENDING); the row's region is complete and only a top-p cut
+// within the streamed normaliser's error bound is open, so the normaliser is
+// recomputed in fp64 and the region finished again (REFINE); the row's
+// region and statistics are written for the region finisher (FINISH; rows
+// computed in several slices are always finished there and carry no mark).
 constexpr int ROW_PENDING = 0x40000000;
 constexpr int ROW_REFINE = 0x40000001;
+constexpr int ROW_FINISH = 0x40000002;
 
 struct SplitStats {       // one per (row, slice), 64 bytes
   double m;               // max of the slice's penalised values (stochastic rows)
@@ -72,7 +74,6 @@ struct SampleArgs {
   int32_t vec_ok;         // rows are 16-byte aligned
   int32_t off_bitmap, off_hword, off_hval, off_dense, off_wkey, off_widx, off_gather;
   int32_t lds_bytes;      // fused kernel dynamic LDS
-  int32_t fin_lds_bytes;  // finish kernel dynamic LDS (several slices per row)
   int32_t bf16;           // logits are bf16 bit patterns
   int32_t f64;            // logits are fp64 (exact multi-pass path only)
   int32_t all_slow;       // every row takes the exact multi-pass path

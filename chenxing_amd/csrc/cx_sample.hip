@@ -22,11 +22,12 @@
 //   * greedy rows: the first argmax over the unpenalised elements (a bitmap
 //     test per vector), merged with the penalised values afterwards.
 //
-// Rows with one slice finish in the same workgroup: top-k rows with a small
-// region are decided by one wave; other rows write their region and
-// statistics and run finish_row (cx_finish.hpp), in the same workgroup or,
-// for several slices, in finish_kernel.  Rows none of these can decide are
-// marked pending and finished by the exact multi-pass kernel (cx_slow.hip).
+// Top-k rows with one slice and a small region are decided in the same
+// workgroup by one wave.  Every other row writes its region and statistics
+// (one record per slice) and is finished by slow_kernel (cx_slow.hip), the
+// launch that follows this one: the region finisher of cx_finish.hpp, then,
+// where that cannot decide, the exact-normaliser refinement or the exact
+// multi-pass path.
 #include "cx_device.hpp"
 #include "cx_sampler.h"
 #include "cx_internal.hpp"
@@ -1028,13 +1029,12 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   wb.tauf = -__builtin_inff();
   wb.overflow = false;
   // Entries a wave keeps: k for top-k rows; otherwise an equal share of the
-  // finisher's sort capacity (in this kernel for one slice per row, in
-  // finish_kernel for several), so the merged region fits in LDS.
-  const int share = max(8, min(KW_MAX, (single ? SORT_CAP : FIN_CAP) / (NWAVE * A.nsplit)));
+  // region finisher's capacity, so the merged region fits in its LDS.
+  const int share = max(8, min(KW_MAX, FIN_CAP / (NWAVE * A.nsplit)));
   wb.kw = P.top_k > 0 ? min(P.top_k, KW_MAX) : share;
   // elements the shared threshold must leave: k of a top-k row, or 1024
   // region entries of a top-p row
-  const int krow = P.top_k > 0 ? P.top_k : SORT_CAP / 2;
+  const int krow = P.top_k > 0 ? P.top_k : FIN_CAP / 4;
   const int pub_r = krow > 64 && krow <= 64 * NWAVE ? (krow + NWAVE - 1) / NWAVE : 0;
   CX_LDS uint32_t* const lslots = to_lds(slots);
   CX_LDS uint32_t* const lpub = to_lds(w_pub);
@@ -1266,22 +1266,12 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
     my->tau = Tf; my->ncand = s_cnt;
     my->flags = (ovf ? SF_OVERFLOW : 0) | (sum_ok ? 0 : SF_INEXACT);
   }
-  // one slice per row: this workgroup finishes the row.  Several slices:
-  // finish_kernel runs after the grid (a kernel boundary makes the slices'
-  // results visible across XCDs without per-workgroup cache writebacks).
-  if (!single) return;
-  __syncthreads();
-  finish_row<SORT_CAP>(A, row, P, dyn, red_d, red_i);
-}
-
-// Finisher for rows computed in several slices: one workgroup per row.
-__global__ __launch_bounds__(WG) void finish_kernel(SampleArgs A) {
-  extern __shared__ __align__(16) unsigned char dyn[];
-  __shared__ double red_d[2 * NWAVE + 4];
-  __shared__ int red_i[2 * NWAVE + 4];
-  const int row = blockIdx.x;
-  const cx_row_params P = A.prm[row];
-  finish_row<FIN_CAP>(A, row, P, dyn, red_d, red_i);
+  // The region finisher runs in slow_kernel, after the grid: a kernel
+  // boundary makes the slices' records visible across XCDs without
+  // per-workgroup cache writebacks, and the finisher's registers stay out of
+  // this kernel.  Sliced rows are always finished there; a single-slice row
+  // is marked.
+  if (single && t == 0) A.row_status[row] = ROW_FINISH;
 }
 
 template __global__ void sample_kernel<false>(SampleArgs);
@@ -1305,16 +1295,6 @@ int launch_sample(const SampleArgs& A, hipStream_t s) {
   else
     timed_launch(CX_KERNEL_SAMPLE, sample_kernel<false>, dim3(A.B * A.nsplit), dim3(WG),
                  A.lds_bytes, s, A);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess || A.nsplit == 1) return (int)e;
-  static int fin_attr = 0;
-  if (A.fin_lds_bytes > fin_attr) {
-    e = hipFuncSetAttribute((const void*)finish_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            A.fin_lds_bytes);
-    if (e != hipSuccess) return (int)e;
-    fin_attr = A.fin_lds_bytes;
-  }
-  timed_launch(CX_KERNEL_SAMPLE_FINISH, finish_kernel, dim3(A.B), dim3(WG), A.fin_lds_bytes, s, A);
   return (int)hipGetLastError();
 }
 }  // namespace cx

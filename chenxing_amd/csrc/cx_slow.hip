@@ -1,11 +1,15 @@
 // cx_slow.hip -- kernels built on the exact multi-pass row path
 // (cx_slow.hpp):
-//   slow_kernel       the rows the fused sampler left pending (or, for fp64
-//                     logits, every row), and the rows it left for
-//                     refinement: their normaliser recomputed exactly in
-//                     fp64, then the region finished again.  One workgroup
-//                     per row; a workgroup whose row is decided reads its
-//                     status word and exits.
+//   slow_kernel       follows every fused launch, one workgroup per row.
+//                     Rows the fused kernel left with a region (every row
+//                     computed in several slices, and single-slice rows
+//                     marked FINISH) get the region finisher; rows it left
+//                     for refinement get their normaliser recomputed
+//                     exactly in fp64 and the region finished again; pending
+//                     rows (or, for fp64 logits, every row) get the exact
+//                     multi-pass path, as does any row the steps before
+//                     cannot decide.  A workgroup whose row is decided reads
+//                     its status word and exits.
 //   penalties_kernel  Sampler.apply_penalties, grid (rows, chunks of PEN_CHUNK)
 //   truncate_kernel   Sampler._truncate, one workgroup per row
 #include "cx_slow.hpp"
@@ -44,18 +48,29 @@ __global__ __launch_bounds__(WG) void slow_kernel(SampleArgs A) {
   __shared__ double red_d[2 * NWAVE + 4];
   __shared__ int red_i[2 * NWAVE + 4];
   __shared__ int s_state;
+  enum { DECIDED, MULTIPASS, REFINE, FINISH };
   const int row = blockIdx.x;
   if (threadIdx.x == 0) {
+    // a sliced row's status word is not written by the fused kernel
     const int st = A.row_status[row];
-    s_state = A.all_slow || st == ROW_PENDING ? 1 : (st == ROW_REFINE ? 2 : 0);
+    s_state = A.all_slow ? MULTIPASS
+              : (A.nsplit > 1 || st == ROW_FINISH) ? FINISH
+              : st == ROW_PENDING ? MULTIPASS
+              : st == ROW_REFINE ? REFINE : DECIDED;
   }
   __syncthreads();
-  const int state = s_state;
-  if (state == 2 && refine_row(A, row, dyn, red_d, red_i)) return;
-  if (state != 0) {
+  int state = s_state;
+  if (state == DECIDED) return;
+  if (state == FINISH) {
+    const cx_row_params P = A.prm[row];
+    const int r = finish_row_fast<FIN_CAP>(A, row, P, dyn, red_d, red_i);
+    if (r == FIN_DONE) return;
+    state = r == FIN_REFINE ? REFINE : MULTIPASS;
     __syncthreads();
-    slow_row(A, row, dyn, red_d, red_i);
   }
+  if (state == REFINE && refine_row(A, row, dyn, red_d, red_i)) return;
+  __syncthreads();
+  slow_row(A, row, dyn, red_d, red_i);
 }
 
 __global__ __launch_bounds__(WG) void penalties_kernel(SampleArgs A) {

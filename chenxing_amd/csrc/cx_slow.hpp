@@ -82,11 +82,14 @@ __device__ __forceinline__ double value_at(const SlowRow& R, int i) {
 }
 
 // sum over the row of exp((x - M) / T), x the penalised fp64 values (the
-// reference's normaliser, sampler.py:119-123), in fp64.  Every thread keeps
-// EXN independent loads in flight per step; the result is the same on every
-// thread.
+// reference's normaliser, sampler.py:119-123), in fp64, with the
+// table-driven exp (within 1 ulp; every argument is <= 0).  Every thread
+// keeps EXN independent loads in flight per step; the result is the same on
+// every thread.
 __device__ inline double exact_norm(const SlowRow& R, double M, double invT, double* red_d) {
   constexpr int EXN = 8;
+  __shared__ double etab[64];
+  load_exp64_tab(etab);
   const int t = threadIdx.x;
   double s = 0.0;
   for (int base = 0; base < R.V; base += EXN * WG) {
@@ -99,7 +102,7 @@ __device__ inline double exact_norm(const SlowRow& R, double M, double invT, dou
 #pragma unroll
     for (int j = 0; j < EXN; ++j) {
       const int i = base + j * WG + t;
-      if (i < R.V) s += exp((penalise_at(R, i, x[j]) - M) * invT);
+      if (i < R.V) s += exp64_neg((penalise_at(R, i, x[j]) - M) * invT, etab);
     }
   }
   return block_sum(s, red_d);

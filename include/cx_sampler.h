@@ -192,10 +192,11 @@ int cx_spec_verify_host(const float* target, const float* draft, const int32_t* 
  * No counterpart in the reference (which has no device code); callers are
  * benchmarks and profilers. */
 #define CX_KERNEL_SAMPLE        0  /* fused sampler kernel            */
-#define CX_KERNEL_SAMPLE_SLOW   1  /* exact multi-pass row kernel     */
+#define CX_KERNEL_SAMPLE_SLOW   1  /* region finisher / exact row kernel */
 #define CX_KERNEL_VERIFY_STATS  2  /* verify: stats over all rows     */
 #define CX_KERNEL_VERIFY_REST   3  /* verify: decide + residual draw  */
-#define CX_KERNEL_SAMPLE_FINISH 4  /* sampler finisher (rows in several slices) */
+#define CX_KERNEL_SAMPLE_FINISH 4  /* reserved: no longer launched (the region
+                                      finisher runs in CX_KERNEL_SAMPLE_SLOW) */
 #define CX_KERNEL_PENALTIES     5  /* apply_penalties                 */
 #define CX_KERNEL_TRUNCATE      6  /* _truncate                       */
 #define CX_KERNEL_KINDS         7

@@ -73,7 +73,7 @@ def test_near_cut_top_k_rows_with_penalties(want_probs):
 
 @pytest.mark.parametrize("want_probs", [False, True])
 def test_near_cut_nucleus_rows_in_slices(want_probs):
-    """Several slices per row (B = 8): finish_kernel hands the row over."""
+    """Several slices per row (B = 8): the region finisher hands the row over."""
     rng = np.random.default_rng(22)
     B, V = 8, 128256
     x = rng.normal(0, 2, (B, V)).astype(np.float32)
