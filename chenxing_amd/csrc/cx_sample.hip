@@ -684,14 +684,15 @@ __device__ __forceinline__ void lean_ranks(const CX_LDS uint64_t* gk, const CX_L
   }
 }
 
-// One wave decides the row from the ranks; Rb and S give probabilities
-// exp2(x c - Rb) / S within tol (relative) of the exact ones.  Returns false
-// when the row needs the exact path (near a top-p boundary, or more than
-// 64 entries tied into the top-k).
 // Outcomes of lean_decide.
 constexpr int LEAN_PENDING = 0;  // the exact multi-pass path must take the row
 constexpr int LEAN_DONE = 1;
 constexpr int LEAN_NEAR = 2;     // a top-p cut within the normaliser's error bound
+
+// One wave decides the row from the ranks; Rb and S give probabilities
+// exp2(x c - Rb) / S within tol (relative) of the exact ones.  LEAN_NEAR
+// sends the row to the exact-normaliser refinement, LEAN_PENDING (more than
+// 64 entries tied into the top-k) to the exact path.
 
 __device__ inline int lean_decide(const cx_row_params& P, const CX_LDS uint64_t* gk,
                                   const CX_LDS int32_t* gi, int nlist, double kc, double Rb,
