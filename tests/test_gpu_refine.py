@@ -90,3 +90,34 @@ def test_nucleus_config_avoids_multipass_path():
     t = compare_rows(ids, st, probs, oracle_rows(w), w.name)
     assert not t.mismatches, t.mismatches[:5]
     assert not np.any(st & FLAG_SLOW), np.flatnonzero(st & FLAG_SLOW)
+
+
+@pytest.mark.parametrize("want_probs", [False, True])
+def test_tied_group_at_the_cut_takes_the_sorting_finisher(want_probs):
+    """200 ids share one value around rank 300 and top_p falls inside that
+    group: the cut's bucket holds more than 64 entries, so the region
+    finisher sorts the region instead (ties in ascending id order)."""
+    rng = np.random.default_rng(23)
+    B, V = 4, 32000
+    x = rng.normal(0, 1, (B, V)).astype(np.float32)
+    prms = []
+    for b in range(B):
+        order = np.argsort(-x[b], kind="stable")
+        tied = rng.choice(order[250:2000], 200, replace=False)
+        x[b, tied] = x[b, order[300]]
+        base = RowParams(temperature=1.0)
+        P = R.tempered_probs(R.penalize(x[b], None, base), 1.0)
+        o = np.argsort(-P, kind="stable")
+        run = np.cumsum(P[o])
+        first = int(np.flatnonzero(P[o] == P[tied[0]])[0])
+        m = first + 60 + 20 * b                      # inside the tied group
+        prms.append(RowParams(temperature=1.0, top_p=float(0.5 * (run[m] + run[m + 1]))))
+    u = rng.random(B)
+    _say(f"[gpu] refine tied group B={B} V={V} probs={want_probs}")
+    ids, st, probs = sample_host(x, prms, None, None, u, want_probs=want_probs)
+    orc = [R.sample_row(x[b], prms[b], None, float(u[b]), tie="stable", keep_probs=want_probs)
+           for b in range(B)]
+    t = compare_rows(ids, st, probs, orc, "tied group")
+    assert not t.mismatches, t.mismatches[:5]
+    assert np.array_equal(ids, [o.token for o in orc])
+    assert not np.any(st & FLAG_SLOW), np.flatnonzero(st & FLAG_SLOW)
