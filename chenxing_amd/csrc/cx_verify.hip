@@ -535,6 +535,8 @@ __global__ __launch_bounds__(WG) void verify_draw(VerifyArgs A) {
   __shared__ int red_i[2 * NWAVE + 4];
   __shared__ double tab[64];
   __shared__ double tsum[2 * WG];
+  __shared__ double s_fp[2 * WG];                     // the partials' fp, then ...
+  __shared__ int s_na[2 * WG];                        // ... namb, kept from the first pass
   __shared__ double s_lam[3];
   __shared__ int s_state[2];                          // {0 undecided, 1 token, 2 NaN}, token
   const int b = blockIdx.x;
@@ -563,23 +565,41 @@ __global__ __launch_bounds__(WG) void verify_draw(VerifyArgs A) {
   // leave the row to the block-wide exact redo below.
   if (wave_id() == 0) {
     const int l = lane_id();
+    // one pass over the partials: the sums, and each lane keeps its
+    // sub-chunks' dp, fp and namb in LDS for the residual masses
     double st = 0.0, sq = 0.0;
-    for (int s = l; s < ns; s += 64) { st += np[s].se; sq += np[s].sf; }
+    for (int s = l; s < ns; s += 64) {
+      const NormPart P = np[s];
+      st += P.se;
+      sq += P.sf;
+      tsum[s] = P.dp;
+      s_fp[s] = P.fp;
+      s_na[s] = P.namb;
+    }
     const double St = wave_reduce(st, OpAdd()), Sq = wave_reduce(sq, OpAdd());
     const double lam = St / Sq, lam0 = q.St / q.Sq;
     // residual mass of each sub-chunk: the sure-positive part and the list
+    // (a list's entries are loaded together)
     bool over = false;
     for (int s = l; s < ns; s += 64) {
-      const NormPart P = np[s];
+      const int na = s_na[s];
       double w = 0.0;
-      if (P.namb > AMB_CAP) {
+      if (na > AMB_CAP) {
         over = true;
       } else {
-        w = P.dp - (lam - lam0) * P.fp;
-        const AmbEntry* am = A.amb + ((size_t)b * ns + s) * AMB_CAP;
-        for (int j = 0; j < P.namb; ++j) {
-          const double d = am[j].e - lam * am[j].f;
-          w += d > 0.0 ? d : 0.0;
+        w = tsum[s] - (lam - lam0) * s_fp[s];
+        if (na > 0) {
+          const AmbEntry* am = A.amb + ((size_t)b * ns + s) * AMB_CAP;
+          AmbEntry a[AMB_CAP];
+#pragma unroll
+          for (int j = 0; j < AMB_CAP; ++j)
+            if (j < na) a[j] = am[j];
+#pragma unroll
+          for (int j = 0; j < AMB_CAP; ++j)
+            if (j < na) {
+              const double d = a[j].e - lam * a[j].f;
+              w += d > 0.0 ? d : 0.0;
+            }
         }
       }
       tsum[s] = w;
