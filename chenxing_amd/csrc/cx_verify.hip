@@ -457,8 +457,10 @@ __global__ __launch_bounds__(WG) void verify_norm(VerifyArgs A) {
   const int b = blockIdx.x / NORM_WGS;
   const float T = A.temperature[b];
   const SeqState q = A.seq[b];
-  if (T == 0.0f || q.rej1 == 0) return;
+  // the table is copied before the test, so its load is in flight with the
+  // state's instead of behind it
   load_exp64_tab(tab);
+  if (T == 0.0f || q.rej1 == 0) return;
   const int r = q.rej1 - 1;
   const float* tr = trow(A, b, r);
   const float* dr = drow(A, b, r);
@@ -543,8 +545,8 @@ __global__ __launch_bounds__(WG) void verify_draw(VerifyArgs A) {
   const int t = threadIdx.x;
   const float T = A.temperature[b];
   const SeqState q = A.seq[b];
+  load_exp64_tab(tab);                                // in flight with the state
   if (T == 0.0f || q.rej1 == 0) return;
-  load_exp64_tab(tab);
   const int r = q.rej1 - 1;
   const int g = A.gamma;
   const int ns = A.nsub;                              // <= 2 * WG
