@@ -4,8 +4,10 @@
 // The reference walks the gamma draft positions serially and stops at the
 // first rejection.  Every position's accept test depends only on its own
 // target/draft row pair and its own uniform, so the device evaluates all
-// positions in parallel and then takes the first rejection.  Four launches,
-// each reading what the previous one wrote:
+// positions in parallel and then takes the first rejection.  Stream-ordered
+// launches, each reading what the previous one wrote: 1, 3 and 4 when any
+// sequence is stochastic (the decision, 2, is taken inside each verify_norm
+// workgroup), 1 and 2 when every sequence is greedy:
 //
 //   1. verify_stats   one wave per 2048-element chunk of every target and
 //                     draft row (one HBM read): the chunk max,
@@ -278,17 +280,19 @@ __device__ inline int merge_greedy(const VerifyArgs& A, int r) {
   return ni != INT_MAX ? ni : (key == 0 ? 0 : (int)~(uint32_t)key);
 }
 
-__global__ __launch_bounds__(WG) void verify_decide(VerifyArgs A) {
+// The decision of sequence b (all threads of the workgroup; the same state
+// on every thread): the accept tests, the first rejection, and its row
+// pair's statistics.  `write`: also store the sequence's outputs and its
+// SeqState.  tab: EXP64_TAB in LDS.
+__device__ inline SeqState decide_seq(const VerifyArgs& A, int b, bool write, const double* tab) {
   __shared__ double red_d[2 * NWAVE + 4];
   __shared__ int red_i[2 * NWAVE + 4];
-  __shared__ double tab[64];
   __shared__ float s_M[2 * GAMMA_MAX + 1];
   __shared__ double s_S[2 * GAMMA_MAX + 1];
   __shared__ float s_x[2 * GAMMA_MAX + 1];
   __shared__ int s_best[GAMMA_MAX + 1];
   __shared__ int s_f, s_kind;
-  load_exp64_tab(tab);
-  const int b = blockIdx.x;
+  __shared__ SeqState s_out;
   const int g = A.gamma;
   const int t = threadIdx.x;
   const float T = A.temperature[b];
@@ -307,13 +311,17 @@ __global__ __launch_bounds__(WG) void verify_decide(VerifyArgs A) {
     if (t == 0) {
       int acc = 0;
       while (acc < g && ids[acc] == s_best[acc]) ++acc;
-      A.accepted[b] = acc;
-      A.next_tok[b] = s_best[acc];                    // row gamma: the bonus token
-      A.used[b] = 0;
-      A.row_status[b] = CX_ROW_GREEDY;
-      A.seq[b] = out;
+      if (write) {
+        A.accepted[b] = acc;
+        A.next_tok[b] = s_best[acc];                  // row gamma: the bonus token
+        A.used[b] = 0;
+        A.row_status[b] = CX_ROW_GREEDY;
+        A.seq[b] = out;
+      }
+      s_out = out;
     }
-    return;
+    __syncthreads();
+    return s_out;
   }
   // ids outside [0, V) or missing draft rows cannot be verified: report the
   // sequence as unsupported
@@ -322,11 +330,15 @@ __global__ __launch_bounds__(WG) void verify_decide(VerifyArgs A) {
   bad = block_max(bad, red_i, 0);
   if (bad) {
     if (t == 0) {
-      A.accepted[b] = 0; A.next_tok[b] = -1; A.used[b] = 0;
-      A.row_status[b] = CX_ROW_UNSUPPORTED;
-      A.seq[b] = out;
+      if (write) {
+        A.accepted[b] = 0; A.next_tok[b] = -1; A.used[b] = 0;
+        A.row_status[b] = CX_ROW_UNSUPPORTED;
+        A.seq[b] = out;
+      }
+      s_out = out;
     }
-    return;
+    __syncthreads();
+    return s_out;
   }
   // one wave per row: target rows 0..g-1 at [0, g), draft rows at [g, 2g)
   for (int j = wave_id(); j < 2 * g; j += NWAVE) {
@@ -389,23 +401,38 @@ __global__ __launch_bounds__(WG) void verify_decide(VerifyArgs A) {
     start = f + 1;
   }
   if (t == 0) {
-    if (rej < 0) {                                    // speculative.py:168-171
-      A.accepted[b] = g;
-      A.next_tok[b] = -1;
-      A.used[b] = g;
-      A.row_status[b] = CX_ROW_OK;
-    } else {
+    if (rej >= 0) {
       out.rej1 = rej + 1;
       out.Mt = s_M[rej];
       out.Mq = s_M[g + rej];
       out.St = St;
       out.Sq = Sq;
       out.exact = exact;
-      A.accepted[b] = rej;
-      A.used[b] = rej + 2;                            // tests 0..rej, then the residual draw
     }
-    A.seq[b] = out;
+    if (write) {
+      if (rej < 0) {                                  // speculative.py:168-171
+        A.accepted[b] = g;
+        A.next_tok[b] = -1;
+        A.used[b] = g;
+        A.row_status[b] = CX_ROW_OK;
+      } else {
+        A.accepted[b] = rej;
+        A.used[b] = rej + 2;                          // tests 0..rej, then the residual draw
+      }
+      A.seq[b] = out;
+    }
+    s_out = out;
   }
+  __syncthreads();
+  return s_out;
+}
+
+// Batches whose sequences are all greedy: the decision alone, one workgroup
+// per sequence.
+__global__ __launch_bounds__(WG) void verify_decide(VerifyArgs A) {
+  __shared__ double tab[64];
+  load_exp64_tab(tab);
+  decide_seq(A, blockIdx.x, true, tab);
 }
 
 // ------------------------------------------------------------ 3. normaliser partials
@@ -455,11 +482,11 @@ __device__ __forceinline__ void pair_terms(const float (&xt)[8], const float (&x
 __global__ __launch_bounds__(WG) void verify_norm(VerifyArgs A) {
   __shared__ double tab[64];
   const int b = blockIdx.x / NORM_WGS;
-  const float T = A.temperature[b];
-  const SeqState q = A.seq[b];
-  // the table is copied before the test, so its load is in flight with the
-  // state's instead of behind it
   load_exp64_tab(tab);
+  // every workgroup of the sequence takes the decision itself (a launch
+  // less than a separate decide kernel); the first one stores it
+  const SeqState q = decide_seq(A, b, blockIdx.x % NORM_WGS == 0, tab);
+  const float T = A.temperature[b];
   if (T == 0.0f || q.rej1 == 0) return;
   const int r = q.rej1 - 1;
   const float* tr = trow(A, b, r);
@@ -708,10 +735,12 @@ int launch_verify(const VerifyArgs& A, bool any_stochastic, hipStream_t s) {
   const int nrows = nt + (any_stochastic ? A.B * A.gamma : 0);
   const int per_row = (A.nchunk + NWAVE - 1) / NWAVE;
   timed_launch(CX_KERNEL_VERIFY_STATS, verify_stats, dim3(nrows * per_row), dim3(WG), 0, s, A);
-  timed_launch(CX_KERNEL_VERIFY_REST, verify_decide, dim3(A.B), dim3(WG), 0, s, A);
   if (any_stochastic) {
+    // verify_norm takes the decision in each of its workgroups
     timed_launch(CX_KERNEL_VERIFY_REST, verify_norm, dim3(A.B * NORM_WGS), dim3(WG), 0, s, A);
     timed_launch(CX_KERNEL_VERIFY_REST, verify_draw, dim3(A.B), dim3(WG), 0, s, A);
+  } else {
+    timed_launch(CX_KERNEL_VERIFY_REST, verify_decide, dim3(A.B), dim3(WG), 0, s, A);
   }
   return (int)hipGetLastError();
 }
