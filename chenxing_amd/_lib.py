@@ -203,16 +203,27 @@ def spec_verify_host(target: np.ndarray, draft: np.ndarray | None, draft_ids: np
 
 # ------------------------------------------------------------------ device entry points
 class Workspace:
-    """A zero-filled device scratch buffer, grown on demand (one per stream)."""
+    """Zero-filled device scratch buffers, one per (device, stream), grown on
+    demand.  The library's calls on one stream run in order and can share a
+    buffer; calls on different streams (or from threads using different
+    streams) must not, since each call's kernels use the buffer for the
+    rows' regions and statistics.  A buffer is allocated on the stream it
+    serves, so replacing it with a larger one is ordered after the calls
+    already queued there."""
 
     def __init__(self):
-        self.buf = None
+        self.bufs: dict = {}
+        self.lock = threading.Lock()
 
-    def get(self, nbytes: int, device):
+    def get(self, nbytes: int, device, stream_ptr: int):
         import torch
-        if self.buf is None or self.buf.numel() < nbytes or self.buf.device != device:
-            self.buf = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
-        return self.buf
+        key = (device.index, stream_ptr)
+        with self.lock:
+            buf = self.bufs.get(key)
+            if buf is None or buf.numel() < nbytes:
+                buf = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
+                self.bufs[key] = buf
+            return buf
 
 
 _ws_sample = Workspace()
@@ -244,7 +255,8 @@ def sample_device(logits, prm, u, hist=None, hist_len=None, out_id=None, row_sta
         row_status = torch.empty(B, dtype=torch.int32, device=dev)
     ldh = 0 if hist is None else hist.shape[1]
     nbytes = lib.cx_sample_workspace_bytes(B, V, ldh)
-    ws = _ws_sample.get(nbytes, dev)
+    sp = _stream_ptr(dev)
+    ws = _ws_sample.get(nbytes, dev, sp.value)
     fns = {torch.bfloat16: lib.cx_sample_bf16, torch.float32: lib.cx_sample_f32,
            torch.float64: lib.cx_sample_f64}
     if logits.dtype not in fns:
@@ -256,7 +268,7 @@ def sample_device(logits, prm, u, hist=None, hist_len=None, out_id=None, row_sta
               _P(prm.data_ptr()), _P(u.data_ptr()), _P(out_id.data_ptr()),
               _P(row_status.data_ptr()),
               _P(out_probs.data_ptr()) if out_probs is not None else None,
-              _P(ws.data_ptr()), ws.numel(), _stream_ptr(dev)))
+              _P(ws.data_ptr()), ws.numel(), sp))
     return out_id, row_status
 
 
@@ -271,11 +283,12 @@ def spec_verify_device(target, draft, draft_ids, u, temperature, accepted=None, 
     outs = [x if x is not None else torch.empty(B, dtype=torch.int32, device=dev)
             for x in (accepted, next_tok, used, row_status)]
     nbytes = lib.cx_spec_verify_workspace_bytes(B, g, V)
-    ws = _ws_verify.get(nbytes, dev)
+    sp = _stream_ptr(dev)
+    ws = _ws_verify.get(nbytes, dev, sp.value)
     _check(lib.cx_spec_verify_f32(
         _P(target.data_ptr()), _P(draft.data_ptr()) if draft is not None else None,
         _P(draft_ids.data_ptr()), _P(u.data_ptr()), _P(temperature.data_ptr()), B, g, V,
-        *[_P(o.data_ptr()) for o in outs], _P(ws.data_ptr()), ws.numel(), _stream_ptr(dev)))
+        *[_P(o.data_ptr()) for o in outs], _P(ws.data_ptr()), ws.numel(), sp))
     return tuple(outs)
 
 

@@ -254,6 +254,39 @@ def test_device_tensor_input_matches_host_input():
     assert one == host[3]
 
 
+def test_device_calls_on_two_streams_use_their_own_workspaces():
+    """Two batches sampled alternately on two streams with no wait between
+    the calls: each stream's results equal the host call on its batch (the
+    device variant keeps one workspace per device and stream; the sliced
+    top-p rows here fill it with regions and statistics)."""
+    import torch
+    from chenxing_amd import _lib
+    from chenxing_amd.params import RowParams, pack_rows
+    rng = np.random.default_rng(41)
+    B, V = 32, 60000
+    xs = [rng.normal(0, 2, (B, V)).astype(np.float32) for _ in range(2)]
+    prm = [RowParams(temperature=1.0, top_p=0.9) for _ in range(B)]
+    us = [rng.random(B) for _ in range(2)]
+    want = [_lib.sample_host(x, prm, None, None, u)[:2] for x, u in zip(xs, us)]
+    dev = torch.device("cuda:0")
+    packed = torch.from_numpy(pack_rows(prm).view(np.uint8).copy()).to(dev)
+    streams = [torch.cuda.Stream(device=dev), torch.cuda.Stream(device=dev)]
+    xd = [torch.from_numpy(x).to(dev) for x in xs]
+    ud = [torch.from_numpy(u).to(dev) for u in us]
+    torch.cuda.synchronize()
+    _say(f"[gpu] sample_device on two streams B={B} V={V}")
+    outs = [[], []]
+    for _ in range(3):
+        for k in range(2):
+            with torch.cuda.stream(streams[k]):
+                outs[k].append(_lib.sample_device(xd[k], packed, ud[k]))
+    torch.cuda.synchronize()
+    for k in range(2):
+        for ids, st in outs[k]:
+            assert np.array_equal(ids.cpu().numpy(), want[k][0]), k
+            assert np.array_equal(st.cpu().numpy(), want[k][1]), k
+
+
 # ---------------------------------------------- batched row operations at full size
 def test_apply_penalties_full_size_workload():
     """B=256, V=128256 rows with 2048-id Zipf histories, repetition,
