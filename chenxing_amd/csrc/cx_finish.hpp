@@ -373,17 +373,24 @@ __device__ inline int finish_row_fast(const SampleArgs& A, int row, const cx_row
   double* sv = (double*)(dyn + CAP * 16);
   double* sc = sv + CAP;
 
-  if (t == 0) f_n = 0;
+  // the slices' candidates as one list (prefix of their counts), so their
+  // loads go out together rather than one slice after another
+  __shared__ int f_off[SLICE_CAP + 1];
+  if (t == 0) {
+    int o = 0;
+    for (int s = 0; s < nsp; ++s) { f_off[s] = o; o += st[s].ncand; }
+    f_off[nsp] = o;
+    f_n = 0;
+  }
   __syncthreads();
-  for (int s = 0; s < nsp; ++s) {
-    const Cand* cs = A.cands + ((size_t)row * nsp + s) * CAPS;
-    const int n = st[s].ncand;
-    for (int e = t; e < n; e += WG) {
-      Cand c = cs[e];
-      if (c.key >= thr64) {
-        int pos = atomicAdd(&f_n, 1);
-        if (pos < CAP) { skey[pos] = c.key; sidx[pos] = c.idx; saux[pos] = 0; }
-      }
+  const int ncand = f_off[nsp];
+  for (int g = t; g < ncand; g += WG) {
+    int s = 0;
+    while (g >= f_off[s + 1]) ++s;
+    const Cand c = A.cands[((size_t)row * nsp + s) * CAPS + (g - f_off[s])];
+    if (c.key >= thr64) {
+      const int pos = atomicAdd(&f_n, 1);
+      if (pos < CAP) { skey[pos] = c.key; sidx[pos] = c.idx; saux[pos] = 0; }
     }
   }
   __syncthreads();

@@ -158,6 +158,7 @@ struct SampleWorkspace {
 inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
 constexpr int SLICE_MAX = 1 << 18;        // elements per slice (bitmap index limit)
+constexpr int SLICE_CAP = 8;              // slices per row (V < 2^20 needs at most 4)
 
 // Slices per row: one when the batch alone fills the 256 CUs (no cross-
 // workgroup merge at all); otherwise enough slices for about 512 workgroups,
@@ -166,7 +167,7 @@ inline int choose_nsplit(int B, int V) {
   int n = B >= 256 ? 1 : (512 + B - 1) / (B > 0 ? B : 1);
   int by_len = V / 16384 > 0 ? V / 16384 : 1;
   if (n > by_len) n = by_len;
-  if (n > 8) n = 8;
+  if (n > SLICE_CAP) n = SLICE_CAP;
   int need = (V + SLICE_MAX - 1) / SLICE_MAX;
   if (n < need) n = need;
   return n < 1 ? 1 : n;
