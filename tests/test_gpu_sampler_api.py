@@ -254,6 +254,27 @@ def test_device_tensor_input_matches_host_input():
     assert one == host[3]
 
 
+def test_bf16_device_tensor_matches_the_host_variant():
+    """A torch.bfloat16 batch on the device (the large-vocabulary
+    heterogeneous workload's rows: per-row temperature, top-k and top-p,
+    greedy rows) gives the host variant's ids and statuses on the same bf16
+    bits; the host variant is checked against the oracle elsewhere."""
+    import torch
+    from chenxing_amd import _lib, workloads as W
+    from chenxing_amd.params import pack_rows
+    w = W.hetero_bf16(B=64)
+    _say(f"[gpu] bf16 device tensor {w.name} B={w.B} V={w.V}")
+    ids_h, st_h, _ = _lib.sample_host(w.logits, w.params, None, None, w.u, bf16=True)
+    dev = torch.device("cuda:0")
+    x = torch.from_numpy(w.logits.view(np.int16)).to(dev).view(torch.bfloat16)
+    prm = torch.from_numpy(pack_rows(w.params).view(np.uint8).copy()).to(dev)
+    u = torch.from_numpy(np.ascontiguousarray(w.u, dtype=np.float64)).to(dev)
+    ids_d, st_d = _lib.sample_device(x, prm, u)
+    torch.cuda.synchronize()
+    assert np.array_equal(ids_d.cpu().numpy(), ids_h)
+    assert np.array_equal(st_d.cpu().numpy(), st_h)
+
+
 def test_device_calls_on_two_streams_use_their_own_workspaces():
     """Two batches sampled alternately on two streams with no wait between
     the calls: each stream's results equal the host call on its batch (the
