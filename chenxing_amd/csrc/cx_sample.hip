@@ -1033,9 +1033,11 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   // region finisher's capacity, so the merged region fits in its LDS.
   const int share = max(8, min(KW_MAX, FIN_CAP / (NWAVE * A.nsplit)));
   wb.kw = P.top_k > 0 ? min(P.top_k, KW_MAX) : share;
-  // elements the shared threshold must leave: k of a top-k row, or 1024
-  // region entries of a top-p row
-  const int krow = P.top_k > 0 ? P.top_k : FIN_CAP / 4;
+  // elements the shared threshold must leave: k of a top-k row, or for a
+  // top-p row 1024 region entries, or the slice's share of the finisher's
+  // capacity if that is less (a lower first threshold only adds appends and
+  // compactions)
+  const int krow = P.top_k > 0 ? P.top_k : min(FIN_CAP / 4, NWAVE * share);
   const int pub_r = krow > 64 && krow <= 64 * NWAVE ? (krow + NWAVE - 1) / NWAVE : 0;
   CX_LDS uint32_t* const lslots = to_lds(slots);
   CX_LDS uint32_t* const lpub = to_lds(w_pub);
