@@ -1,8 +1,10 @@
-// cx_finish.hpp -- per-row finisher of the fused sampler.
+// cx_finish.hpp -- region finisher of the fused sampler.
 //
-// Runs in the last workgroup of a row.  Merges the slices' statistics,
-// gathers the exact region into LDS, sorts it, and applies the reference's
-// filters on fp64 probabilities:
+// Runs in slow_kernel, one workgroup per row, after the fused kernel has
+// written the row's statistics and region (one record per slice).  Merges
+// the slices' statistics, gathers the exact region into LDS, and applies
+// the reference's filters on fp64 probabilities, with bucketed cuts (a
+// sort of the whole region only when a cut's bucket overflows):
 //   top-k   sampler.py:76-79  keep every value >= the k-th largest
 //   top-p   sampler.py:81-89  shortest prefix (value desc, id asc) with cum >= p
 //   min-p   sampler.py:91-93  keep P >= min_p * max P
