@@ -81,6 +81,21 @@ def test_near_cut_nucleus_rows_in_slices(want_probs):
     _check_exact(x, prms, None, rng.random(B), want_probs, "nucleus near cut")
 
 
+@pytest.mark.parametrize("want_probs", [False, True])
+def test_near_cut_sliced_rows_with_penalties(want_probs):
+    """Sliced rows (B = 8) with 512-id Zipf histories and repetition,
+    presence and frequency penalties: the exact normaliser applies the
+    penalties as the stream did."""
+    rng = np.random.default_rng(24)
+    B, V, H = 8, 128256, 512
+    x = rng.normal(0, 2, (B, V)).astype(np.float32)
+    hist = W.zipf_history(rng, B, H, V).astype(np.int32)
+    kw = dict(temperature=0.9, repetition_penalty=1.3, presence_penalty=0.4,
+              frequency_penalty=0.2)
+    prms = _near_cut_rows(rng, x, hist, kw, 100, 800)
+    _check_exact(x, prms, hist, rng.random(B), want_probs, "sliced near cut, penalties")
+
+
 def test_nucleus_config_avoids_multipass_path():
     """B = 64 top-p 0.95 rows: every nucleus fits the sliced region and the
     rows near the cut are refined, so no row takes the multi-pass path."""
