@@ -72,6 +72,54 @@ static void slow_layout(SampleArgs& A, int32_t V, int64_t ldh) {
   A.slow_lds_bytes = (int)so;
 }
 
+constexpr int FUSED_LDS_MAX = 150 * 1024;   // fused kernel dynamic LDS (static LDS comes on top)
+
+static int split_len_of(int V, int nsplit) {
+  const int per = (V + nsplit - 1) / nsplit;
+  return (per + 7) / 8 * 8;
+}
+
+// Dynamic LDS layout of the fused kernel for A.split_len and A.ns: the
+// penalty index (bitmap of the slice's window ids, hash of (id << 12 | count)
+// words, the ids' raw logits and the dense list of occupied slots) and the
+// per-wave candidate buffers.
+static void fused_layout(SampleArgs& A, int64_t ldh) {
+  const long nbw = ldh > 0 ? (A.split_len + 31) / 32 : 0;
+  const long nslot = ldh > 0 ? A.ns : 0;
+  size_t off = 0;
+  A.off_bitmap = 0;
+  off = align_up((size_t)nbw * 4, 16);
+  A.off_hword = (int)off;
+  off += (size_t)nslot * 4;
+  A.off_hval = (int)off;
+  off += (size_t)nslot * 4;
+  A.off_dense = (int)off;
+  off = align_up(off + (size_t)nslot * 4, 16);
+  A.off_wkey = (int)off;
+  off += (size_t)16 * CAPW * 4;
+  A.off_widx = (int)off;
+  off += (size_t)16 * CAPW * 4;
+  A.off_gather = (int)off;
+  off += (size_t)LEAN_CAP * 12;
+  A.lds_bytes = (int)off;
+}
+
+// Slices per row: choose_nsplit's, raised while the fused kernel's LDS
+// layout does not fit (its penalty bitmap covers one slice, so a long
+// vocabulary with a long history window needs shorter slices).  At
+// SLICE_CAP slices every layout fits for V < 2^20.
+static int plan_nsplit(int B, int V, int64_t ldh) {
+  SampleArgs A;
+  memset(&A, 0, sizeof A);
+  slow_layout(A, V, ldh);
+  int n = choose_nsplit(B, V);
+  for (;; ++n) {
+    A.split_len = split_len_of(V, n);
+    fused_layout(A, ldh);
+    if (A.lds_bytes <= FUSED_LDS_MAX || n >= SLICE_CAP) return n;
+  }
+}
+
 // dtype: 0 fp32, 1 bf16, 2 fp64 (every row on the exact multi-pass path).
 static int sample_impl(const void* logits, int dtype, int64_t ld, int32_t B, int32_t V,
                        const int32_t* hist, const int32_t* hist_len, int64_t ldh,
@@ -87,7 +135,8 @@ static int sample_impl(const void* logits, int dtype, int64_t ld, int32_t B, int
   if (!logits || !prm || !u || !out_id || !row_status || !ws)
     return fail(CX_EINVAL, "null pointer argument");
   if (ldh > 0 && (!hist || !hist_len)) return fail(CX_EINVAL, "history pointers are null");
-  const SampleWorkspace L = sample_workspace_layout(B, V);
+  const int nsplit = plan_nsplit(B, V, ldh);
+  const SampleWorkspace L = sample_workspace_layout(B, nsplit);
   if (ws_bytes < L.total)
     return fail(CX_ENOSPACE, "workspace needs %zu bytes, got %zu", L.total, ws_bytes);
 
@@ -109,9 +158,8 @@ static int sample_impl(const void* logits, int dtype, int64_t ld, int32_t B, int
   A.counters = (int32_t*)(w + L.off_counters);
   A.stats = (SplitStats*)(w + L.off_stats);
   A.cands = (Cand*)(w + L.off_cands);
-  A.nsplit = choose_nsplit(B, V);
-  int per = (V + A.nsplit - 1) / A.nsplit;
-  A.split_len = (per + 7) / 8 * 8;
+  A.nsplit = nsplit;
+  A.split_len = split_len_of(V, nsplit);
   A.bf16 = dtype == 1;
   A.f64 = dtype == 2;
   A.all_slow = dtype == 2;
@@ -119,28 +167,9 @@ static int sample_impl(const void* logits, int dtype, int64_t ld, int32_t B, int
   const int esz = dtype == 2 ? 8 : (dtype == 1 ? 2 : 4);
   A.vec_ok = (((uintptr_t)logits) % 16 == 0) && ((ld * esz) % 16 == 0);
   slow_layout(A, V, ldh);
-  // fused kernel: penalty index (bitmap of the slice's window ids, hash of
-  // (id << 12 | count) words, the ids' raw logits and the dense list of
-  // occupied slots) and the per-wave candidate buffers
-  const long nbw = ldh > 0 ? (A.split_len + 31) / 32 : 0;
-  const long nslot = ldh > 0 ? A.ns : 0;
-  size_t off = 0;
-  A.off_bitmap = 0;
-  off = align_up((size_t)nbw * 4, 16);
-  A.off_hword = (int)off;
-  off += (size_t)nslot * 4;
-  A.off_hval = (int)off;
-  off += (size_t)nslot * 4;
-  A.off_dense = (int)off;
-  off = align_up(off + (size_t)nslot * 4, 16);
-  A.off_wkey = (int)off;
-  off += (size_t)16 * CAPW * 4;
-  A.off_widx = (int)off;
-  off += (size_t)16 * CAPW * 4;
-  A.off_gather = (int)off;
-  off += (size_t)LEAN_CAP * 12;
-  A.lds_bytes = (int)off;
-  if (A.lds_bytes > 150 * 1024) return fail(CX_EINVAL, "LDS layout too large (%d)", A.lds_bytes);
+  fused_layout(A, ldh);
+  if (A.lds_bytes > FUSED_LDS_MAX)
+    return fail(CX_EINVAL, "LDS layout too large (%d)", A.lds_bytes);
   hipStream_t s = (hipStream_t)stream;
   int e = 0;
   if (!A.all_slow) {
@@ -272,9 +301,8 @@ int cx_sample_f64(const double* logits, int64_t ld, int32_t B, int32_t V,
 }
 
 size_t cx_sample_workspace_bytes(int32_t B, int32_t V, int64_t ldh) {
-  (void)ldh;
-  if (B <= 0 || V <= 0) return 256;
-  return sample_workspace_layout(B, V).total;
+  if (B <= 0 || V <= 0 || ldh < 0) return 256;
+  return sample_workspace_layout(B, plan_nsplit(B, V, ldh)).total;
 }
 
 int cx_sample_host(const void* logits, int32_t dtype, int64_t ld, int32_t B, int32_t V,

@@ -193,9 +193,8 @@ inline VerifyWorkspace verify_workspace_layout(int B, int gamma, int V) {
   return w;
 }
 
-inline SampleWorkspace sample_workspace_layout(int B, int V) {
+inline SampleWorkspace sample_workspace_layout(int B, int ns) {
   SampleWorkspace w;
-  int ns = choose_nsplit(B, V);
   w.off_counters = 0;
   w.off_stats = align_up((size_t)B * 4, 256);
   w.off_cands = align_up(w.off_stats + (size_t)B * ns * sizeof(SplitStats), 256);

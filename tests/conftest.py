@@ -30,3 +30,20 @@ def lib():
     """The device library, loaded once; GPU tests only."""
     from chenxing_amd import _lib
     return _lib.load()
+
+
+def pytest_terminal_summary(terminalreporter, exitstatus, config):
+    """Per workload: drawing rows whose sampled id differs from the oracle run
+    in numpy's own tie order (the reference on this host), and how many of
+    those are tie straddles at the top-p / typical cut."""
+    parity = sys.modules.get("parity")
+    rates = getattr(parity, "REF_RATES", None) if parity else None
+    if not rates:
+        return
+    tr = terminalreporter
+    tr.write_line("device vs numpy tie order (reference): label draws differ tie-straddle "
+                  "rate straddling-rows margin-cases")
+    for label, r in sorted(rates.items()):
+        d = max(r["draws"], 1)
+        tr.write_line(f"  {label}: {r['draws']} {r['diff']} {r['diff_tie']} "
+                      f"{r['diff'] / d:.2e} {r['straddle']} {r['margin_vs_stable']}")

@@ -1,7 +1,15 @@
 """Sampler parity on the GPU: the HIP library against the oracle on the same
-inputs and uniforms (rules in tests/parity.py)."""
+inputs and uniforms (rules in tests/parity.py).
+
+Every workload runs twice: with ``out_probs`` (which routes every stochastic
+row through the region finisher, so the probabilities can be compared) and
+without it (the production route, the one the benchmark times: single-slice
+top-k rows are finished inside the fused kernel).  Each is compared with the
+oracle in the device's tie order and, for the rate report, in numpy's own
+order (what the reference computes)."""
 from __future__ import annotations
 
+import functools
 import sys
 
 import numpy as np
@@ -12,7 +20,8 @@ from chenxing_amd import workloads as W
 from chenxing_amd._lib import FLAG_SLOW, ROW_UNSUPPORTED, sample_host
 from chenxing_amd.params import RowParams
 from oracle import sampler_ref as R
-from parity import Tally, compare_rows, oracle_rows
+from oracle_pool import oracle_rows_parallel
+from parity import REF_BUDGET, Tally, compare_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -22,47 +31,73 @@ def _say(*a):
     sys.stdout.flush()
 
 
-def _run(w, want_probs=True, rows=None):
-    _say(f"[gpu] sample {w.name} B={w.B} V={w.V} dtype={w.dtype}")
+@functools.lru_cache(maxsize=2)
+def _workload(name, **kw):
+    return getattr(W, name)(**kw)
+
+
+def _run(w, want_probs=True):
+    _say(f"[gpu] sample {w.name} B={w.B} V={w.V} dtype={w.dtype} probs={want_probs}")
     ids, st, probs = sample_host(w.logits, w.params, w.hist if w.hist.size else None,
                                  w.hist_len, w.u, bf16=(w.dtype == "bf16"), want_probs=want_probs)
     return ids, st, probs
 
 
-def _check(w, ids, st, probs, rows=None):
-    rows = list(range(w.B)) if rows is None else rows
-    orc = oracle_rows(w, rows)
-    t = compare_rows(ids[rows], st[rows], None if probs is None else probs[rows], orc, w.name)
+def _check(w, ids, st, probs, label):
+    """Device rows against the oracle in both tie orders; returns the tally."""
+    pairs = oracle_rows_parallel(w, ties=("stable", "numpy"), keep_probs=probs is not None)
+    t = compare_rows(ids, st, probs, [p[0] for p in pairs], label, ref_rows=[p[1] for p in pairs])
+    _say(f"    {label}: draws {t.draws}, margin cases {t.boundary}; vs numpy's order: "
+         f"{t.ref_diff} differ ({t.ref_diff_tie} tie straddles), {t.ref_straddle} straddle")
     assert not t.mismatches, t.mismatches[:5]
+    assert t.boundary <= REF_BUDGET * t.draws + 1e-9 or t.boundary == 0
     return t
+
+
+def _probs_label(name, want_probs):
+    return name + ("+probs" if want_probs else "")
 
 
 def test_small_batch_config():
     w = W.small_batch()
-    ids, st, probs = _run(w)
-    t = _check(w, ids, st, probs)
-    assert t.draws == 4
+    for want_probs in (True, False):
+        ids, st, probs = _run(w, want_probs)
+        t = _check(w, ids, st, probs, _probs_label("small_batch", want_probs))
+        assert t.draws == 4
 
 
-def test_full_penalty_config():
-    w = W.full_penalty()
-    ids, st, probs = _run(w)
-    t = _check(w, ids, st, probs)
+@pytest.mark.parametrize("want_probs", [True, False])
+def test_full_penalty_config(want_probs):
+    w = _workload("full_penalty")
+    ids, st, probs = _run(w, want_probs)
+    t = _check(w, ids, st, probs, _probs_label("full_penalty", want_probs))
     assert t.draws == 256 and t.boundary == 0
 
 
+@pytest.mark.parametrize("want_probs", [True, False])
 @pytest.mark.parametrize("greedy", [True, False])
-def test_nucleus_config(greedy):
-    w = W.nucleus(greedy=greedy)
-    ids, st, probs = _run(w)
-    t = _check(w, ids, st, probs)
+def test_nucleus_config(greedy, want_probs):
+    w = _workload("nucleus", greedy=greedy)
+    ids, st, probs = _run(w, want_probs)
+    t = _check(w, ids, st, probs, _probs_label(w.name, want_probs))
     assert t.rows == 64
 
 
 def test_hetero_bf16_config_subset():
+    """B=96: each row in three slices, probabilities compared."""
     w = W.hetero_bf16(B=96)
-    ids, st, probs = _run(w)
-    _check(w, ids, st, probs)
+    ids, st, probs = _run(w, True)
+    _check(w, ids, st, probs, "hetero_bf16[B=96]+probs")
+
+
+def test_hetero_bf16_config_full_size():
+    """B=1024, V=256000 bf16, the workload's own size: one slice per row, so
+    the one-wave top-k finish, the FINISH hand-off and the refinement of
+    single-slice rows run exactly as the benchmark runs them."""
+    w = _workload("hetero_bf16")
+    ids, st, probs = _run(w, False)
+    t = _check(w, ids, st, None, "hetero_bf16")
+    assert t.rows == 1024 and t.boundary == 0
 
 
 def test_golden_small_rows():
@@ -173,3 +208,25 @@ def test_window_beyond_lds_limit_is_reported():
     ids, st, _ = sample_host(x, prm, hist, np.full(B, H, np.int32), np.full(B, 0.5))
     assert int(st[0]) & 0xFF == ROW_UNSUPPORTED       # 5000-id window
     assert int(st[1]) & 0xFF != ROW_UNSUPPORTED       # last max(64, 100) ids only
+
+
+@pytest.mark.parametrize("freq", [0.0, 0.3])
+def test_long_windows_on_a_long_vocabulary(freq):
+    """4095-id windows (the longest the LDS index holds) at V=256000: the
+    fused kernel's layout then needs shorter slices than the batch alone
+    would pick; every row must still sample as the oracle does."""
+    rng = np.random.default_rng(21)
+    B, V, H = 256, 256000, 4095
+    x = (rng.standard_normal((B, V), dtype=np.float32) * np.float32(2.0))
+    x[np.arange(B), rng.integers(0, V, B)] += np.float32(8.0)
+    hist = rng.integers(0, V, (B, H)).astype(np.int32)
+    hist[:, : H // 2] = rng.integers(0, 5000, (B, H // 2))       # repeated ids too
+    prm = [RowParams(temperature=float(rng.choice([0.0, 0.7, 1.0])),
+                     top_k=int(rng.choice([0, 40])), top_p=float(rng.choice([1.0, 0.9])),
+                     repetition_penalty=1.2, presence_penalty=0.4, frequency_penalty=freq)
+           for _ in range(B)]
+    w = W.SampleWorkload(f"long_window_f{freq}", x, "f32", prm, hist,
+                         np.full(B, H, np.int32), rng.random(B))
+    ids, st, _ = _run(w, False)
+    t = _check(w, ids, st, None, w.name)
+    assert t.boundary == 0

@@ -18,30 +18,10 @@ from chenxing_amd.params import SamplingParams
 from chenxing_amd.speculative import SpeculativeDecoder
 from oracle import sampler_ref as R
 from oracle import speculative_ref as S
+from oracle_api import OracleSampler
 
 with open(cases.__file__.replace("cases.py", "spec_golden.json")) as f:
     GOLD = json.load(f)
-
-
-class OracleSampler:
-    """``Sampler.sample`` semantics on the oracle (seeded rows only)."""
-
-    def __init__(self, V):
-        self.vocab_size = V
-        self._rng = np.random.default_rng()
-
-    def sample(self, logits, params, generated_ids=None):
-        prm = R.RowParams(temperature=params.temperature, top_k=params.top_k,
-                          top_p=params.top_p, min_p=params.min_p, typical_p=params.typical_p,
-                          repetition_penalty=params.repetition_penalty, n_keep=params.n_keep)
-        g = self._rng if params.seed is None else np.random.default_rng(params.seed)
-        st = g.bit_generator.state
-        res = R.sample_row(logits, prm, generated_ids or [], g.random())
-        if res.status != R.STATUS_OK:
-            g.bit_generator.state = st
-        if res.status == R.STATUS_ERROR:
-            raise ValueError("probabilities contain NaN")
-        return res.token
 
 
 def oracle_verifier(target, draft, ids, u, T):
