@@ -258,7 +258,11 @@ def test_bf16_device_tensor_matches_the_host_variant():
     """A torch.bfloat16 batch on the device (the large-vocabulary
     heterogeneous workload's rows: per-row temperature, top-k and top-p,
     greedy rows) gives the host variant's ids and statuses on the same bf16
-    bits; the host variant is checked against the oracle elsewhere."""
+    bits; the host variant is checked against the oracle elsewhere.  Only
+    the outcome byte of the status is compared: the route flags (refined
+    normaliser, exact multi-pass path) depend on how far each wave's region
+    threshold had risen when the stream ended, which varies with the order
+    the waves publish in; both routes give the exact token."""
     import torch
     from chenxing_amd import _lib, workloads as W
     from chenxing_amd.params import pack_rows
@@ -272,7 +276,7 @@ def test_bf16_device_tensor_matches_the_host_variant():
     ids_d, st_d = _lib.sample_device(x, prm, u)
     torch.cuda.synchronize()
     assert np.array_equal(ids_d.cpu().numpy(), ids_h)
-    assert np.array_equal(st_d.cpu().numpy(), st_h)
+    assert np.array_equal(st_d.cpu().numpy() & 0xFF, st_h & 0xFF)
 
 
 def test_device_calls_on_two_streams_use_their_own_workspaces():
@@ -305,7 +309,7 @@ def test_device_calls_on_two_streams_use_their_own_workspaces():
     for k in range(2):
         for ids, st in outs[k]:
             assert np.array_equal(ids.cpu().numpy(), want[k][0]), k
-            assert np.array_equal(st.cpu().numpy(), want[k][1]), k
+            assert np.array_equal(st.cpu().numpy() & 0xFF, want[k][1] & 0xFF), k
 
 
 # ---------------------------------------------- batched row operations at full size
