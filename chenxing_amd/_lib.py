@@ -33,6 +33,8 @@ _SIGS = {
     "cx_sample_f64": (C.c_int, [_P, C.c_int64, C.c_int32, C.c_int32, _P, _P, C.c_int64, _P, _P,
                                 _P, _P, _P, _P, C.c_size_t, _P]),
     "cx_sample_workspace_bytes": (C.c_size_t, [C.c_int32, C.c_int32, C.c_int64]),
+    "cx_sample_f32_noalloc": (C.c_int, [_P, C.c_int64, C.c_int32, C.c_int32, _P, _P, C.c_int64,
+                                        _P, _P, _P, _P, _P, _P]),
     "cx_apply_penalties": (C.c_int, [_P, C.c_int32, C.c_int64, C.c_int32, C.c_int32, _P, _P,
                                      C.c_int64, _P, _P, C.c_int64, _P, _P]),
     "cx_apply_penalties_host": (C.c_int, [_P, C.c_int32, C.c_int64, C.c_int32, C.c_int32, _P,
@@ -269,6 +271,33 @@ def sample_device(logits, prm, u, hist=None, hist_len=None, out_id=None, row_sta
               _P(row_status.data_ptr()),
               _P(out_probs.data_ptr()) if out_probs is not None else None,
               _P(ws.data_ptr()), ws.numel(), sp))
+    return out_id, row_status
+
+
+def sample_device_noalloc(logits, prm, u, hist=None, hist_len=None, out_id=None,
+                          row_status=None, out_probs=None):
+    """``sample_device`` for float32 logits through ``cx_sample_f32_noalloc``:
+    the library's static per-GPU scratch serves as the workspace, so the call
+    allocates no device memory (the caller passes ``out_id`` and
+    ``row_status`` to allocate nothing at all).  Calls that overlap on one
+    GPU race on that scratch."""
+    import torch
+    lib = load()
+    if logits.dim() != 2 or logits.stride(1) != 1 or logits.dtype != torch.float32:
+        raise ValueError("logits must be a float32 [B, V] tensor with unit column stride")
+    B, V = logits.shape
+    dev = logits.device
+    if out_id is None:
+        out_id = torch.empty(B, dtype=torch.int32, device=dev)
+    if row_status is None:
+        row_status = torch.empty(B, dtype=torch.int32, device=dev)
+    ldh = 0 if hist is None else hist.shape[1]
+    _check(lib.cx_sample_f32_noalloc(
+        _P(logits.data_ptr()), logits.stride(0), B, V,
+        _P(hist.data_ptr()) if hist is not None else None,
+        _P(hist_len.data_ptr()) if hist_len is not None else None, ldh,
+        _P(prm.data_ptr()), _P(u.data_ptr()), _P(out_id.data_ptr()), _P(row_status.data_ptr()),
+        _P(out_probs.data_ptr()) if out_probs is not None else None, _stream_ptr(dev)))
     return out_id, row_status
 
 

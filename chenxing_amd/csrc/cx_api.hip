@@ -4,6 +4,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
+#include <mutex>
 #include <string>
 
 #include "cx_sampler.h"
@@ -268,6 +269,38 @@ struct DevBuf {
   hipError_t alloc(size_t n) { return hipMalloc(&p, n > 0 ? n : 1); }
 };
 
+// ------------------------------------------------------------ static scratch
+// The workspace of cx_sample_f32_noalloc: a file-scope device array (each
+// GPU holds its own copy until the process ends).  Its host-side name is
+// not a device address; the address is looked up once per device with
+// hipGetSymbolAddress and only that address reaches kernels.
+constexpr size_t NOALLOC_SCRATCH_BYTES = CX_NOALLOC_SCRATCH_BYTES;
+constexpr int NOALLOC_MAX_DEVICES = 64;
+static __device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[NOALLOC_MAX_DEVICES];
+
+// The current device's scratch address, looked up on the first call on that
+// device (with the device current, as hipGetSymbolAddress requires).
+static int scratch_of_current_device(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  if (dev < 0 || dev >= NOALLOC_MAX_DEVICES)
+    return fail(CX_EINVAL, "device %d beyond the %d the static scratch serves", dev,
+                NOALLOC_MAX_DEVICES);
+  std::lock_guard<std::mutex> g(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    if (!p) return fail(CX_EHIP, "hipGetSymbolAddress(scratch) returned a null address");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return CX_OK;
+}
+
 }  // namespace cx
 
 using namespace cx;
@@ -280,6 +313,25 @@ int cx_sample_f32(const float* logits, int64_t ld, int32_t B, int32_t V, const i
                   size_t ws_bytes, void* stream) {
   return sample_impl(logits, 0, ld, B, V, hist, hist_len, ldh, prm, u, out_id, row_status,
                      out_probs, workspace, ws_bytes, stream);
+}
+
+int cx_sample_f32_noalloc(const float* logits, int64_t ld, int32_t B, int32_t V,
+                          const int32_t* hist, const int32_t* hist_len, int64_t ldh,
+                          const cx_row_params* prm, const double* u, int32_t* out_id,
+                          int32_t* row_status, float* out_probs, void* stream) {
+  g_err.clear();
+  if (B < 0 || V < 1 || ldh < 0)
+    return fail(CX_EINVAL, "bad shape: B=%d V=%d ldh=%lld", B, V, (long long)ldh);
+  if (B == 0) return CX_OK;
+  if (V >= (1 << 20)) return fail(CX_EINVAL, "V=%d exceeds the 2^20 token-id limit", V);
+  const size_t need = sample_workspace_layout(B, plan_nsplit(B, V, ldh)).total;
+  if (need > NOALLOC_SCRATCH_BYTES)
+    return fail(CX_EINVAL, "B=%d V=%d ldh=%lld needs %zu bytes of scratch; the static scratch "
+                "holds %zu", B, V, (long long)ldh, need, NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  if (int rc = scratch_of_current_device(&ws)) return rc;
+  return sample_impl(logits, 0, ld, B, V, hist, hist_len, ldh, prm, u, out_id, row_status,
+                     out_probs, ws, NOALLOC_SCRATCH_BYTES, stream);
 }
 
 int cx_sample_bf16(const uint16_t* logits, int64_t ld, int32_t B, int32_t V,

@@ -102,6 +102,27 @@ int cx_sample_f64(const double* logits, int64_t ld, int32_t B, int32_t V,
 
 size_t cx_sample_workspace_bytes(int32_t B, int32_t V, int64_t ldh);
 
+/*
+ * cx_sample_f32 without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference, which
+ * has no device code.  It allocates nothing: its workspace is a static
+ * device array of 64 MiB (CX_NOALLOC_SCRATCH_BYTES) that each GPU the
+ * library runs on holds until the process ends.  Inputs, outputs, results
+ * and errors are cx_sample_f32's; a batch whose workspace
+ * (cx_sample_workspace_bytes) exceeds the scratch returns CX_EINVAL before
+ * any device work.  Every call on one GPU shares that GPU's scratch: calls
+ * that overlap on one GPU (on different streams or threads) race and must
+ * be serialised by the caller.  No state carries from one call to the next.
+ */
+#define CX_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int cx_sample_f32_noalloc(const float* logits, int64_t ld, int32_t B, int32_t V,
+                          const int32_t* hist, const int32_t* hist_len, int64_t ldh,
+                          const cx_row_params* prm, const double* u,
+                          int32_t* out_id, int32_t* row_status, float* out_probs,
+                          void* stream);
+
+
 /* Host-memory variants: same arguments on host memory; allocate, copy,
  * launch, copy back and synchronise.  dtype: 0 = fp32, 1 = bf16, 2 = fp64. */
 int cx_sample_host(const void* logits, int32_t dtype, int64_t ld, int32_t B, int32_t V,

@@ -77,3 +77,16 @@ def test_bad_arguments_fail_before_any_device_work():
     # B == 0 is a no-op
     assert lib.cx_sample_f32(None, 8, 0, 8, None, None, 0, None, None, None, None, None, None,
                              0, None) == 0
+
+
+def test_noalloc_refuses_a_batch_beyond_its_static_scratch():
+    """cx_sample_f32_noalloc checks the workspace the batch needs against its
+    64 MiB static scratch before any device call (null pointers: nothing is
+    touched)."""
+    lib = _lib.load()
+    assert lib.cx_sample_workspace_bytes(1024, 256000, 0) > (64 << 20)
+    rc = lib.cx_sample_f32_noalloc(None, 256000, 1024, 256000, None, None, 0, None, None, None,
+                                   None, None, None)
+    assert rc == _lib.CX_EINVAL and b"static scratch" in lib.cx_last_error()
+    assert lib.cx_sample_f32_noalloc(None, 8, 0, 8, None, None, 0, None, None, None, None, None,
+                                     None) == 0
