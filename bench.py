@@ -19,7 +19,9 @@ already resident in HBM.  A step is one cx_sample_f32 call over the batch.
                process pool of up to 16 workers (cpu_baseline_pool)
 
 The other workloads (nucleus, speculative verify, heterogeneous bf16) are
-timed the same way and reported under "other_workloads".
+timed the same way and reported under "other_workloads"; "host_calls" times
+the drop-in Sampler on numpy rows as the reference's engine calls it
+(copies to and from the device included).
 """
 from __future__ import annotations
 
@@ -236,6 +238,45 @@ def time_other(name: str, dev, steps: int, warmup: int) -> dict:
     return entry
 
 
+def time_host_calls(w, calls: int, warmup: int) -> dict:
+    """The drop-in ``Sampler`` as the reference's callers use it: ``sample`` on
+    one numpy row per call (engine.py:165), and ``sample_batch`` on the whole
+    numpy batch.  Each call copies its rows and histories to the device, runs
+    both launches and copies the ids back (PCIe-inclusive, host timer)."""
+    from dataclasses import asdict
+    from chenxing_amd import Sampler, SamplingParams
+    n = min(w.B, 16)
+    s = Sampler(w.V)
+    rows = [np.ascontiguousarray(w.logits[b]) for b in range(n)]
+    ps = [SamplingParams(**asdict(w.params[b])) for b in range(n)]
+    hl = [[int(i) for i in w.hist[b, :w.hist_len[b]]] for b in range(n)]
+    for i in range(warmup):
+        s.sample(rows[i % n], ps[i % n], hl[i % n])
+    ts = []
+    for i in range(calls):
+        t0 = time.perf_counter()
+        s.sample(rows[i % n], ps[i % n], hl[i % n])
+        ts.append(time.perf_counter() - t0)
+    ts.sort()
+    one = {"median_us": round(1e6 * ts[len(ts) // 2], 1),
+           "p90_us": round(1e6 * ts[(9 * len(ts)) // 10], 1), "calls": calls,
+           "note": f"Sampler.sample on one numpy fp32 row (V={w.V}, {w.hist.shape[1]}-id "
+                   "history, all three penalties), copies and both launches included"}
+    bp = [SamplingParams(**asdict(p)) for p in w.params]
+    bh = [[int(i) for i in w.hist[b, :w.hist_len[b]]] for b in range(w.B)]
+    s.sample_batch(w.logits, bp, bh)
+    tb = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        s.sample_batch(w.logits, bp, bh)
+        tb.append(time.perf_counter() - t0)
+    tb.sort()
+    batch = {"median_ms": round(1e3 * tb[2], 3), "rows_per_s": round(w.B / tb[2], 1),
+             "note": f"Sampler.sample_batch on the numpy [{w.B}, {w.V}] batch: the "
+                     "PCIe-inclusive rate of the host-memory entry point"}
+    return {"sample": one, "sample_batch": batch}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -307,6 +348,11 @@ def main() -> int:
                 "slow_path": int(np.sum((st & 0x100) != 0)),
                 "other": int(np.sum((st & 0xFF) != _lib.ROW_OK))}
 
+    host = None
+    if not args.quick:
+        _say("[bench] drop-in Sampler calls on numpy rows")
+        host = time_host_calls(w, 200, 20)
+
     other = {}
     if not args.quick:
         for name in OTHER:
@@ -354,6 +400,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "cpu_baseline_pool": cpu_pool,
         "row_outcomes": outcomes,
+        "host_calls": host,
         "other_workloads": other,
     }
     prof = os.path.join(HERE, "profiles", "sample_kernel_full_penalty_traffic.json")

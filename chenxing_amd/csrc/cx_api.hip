@@ -6,6 +6,7 @@
 #include <string.h>
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "cx_sampler.h"
 #include "cx_device.hpp"
@@ -260,14 +261,130 @@ static int verify_impl(const float* target, const float* draft, const int32_t* i
   return CX_OK;
 }
 
-// Device buffer that frees itself.
-struct DevBuf {
-  void* p = nullptr;
-  ~DevBuf() {
-    if (p) (void)hipFree(p);
-  }
-  hipError_t alloc(size_t n) { return hipMalloc(&p, n > 0 ? n : 1); }
+// ------------------------------------------------------------ host-call arenas
+// Device memory of the host-memory entry points, reused from call to call so
+// that a call allocates only when it needs more than any call before it on
+// that arena.  One arena per concurrent caller and device: a call takes an
+// idle arena of the current device (or makes one) and returns it when done.
+// Arenas are held until the process ends; freeing them from a static
+// destructor could run after the HIP runtime has shut down.  Each arena has
+// its own stream (default priority), so a host call waits only for its own
+// copies and kernels.  The workspace part is zero-filled when it is
+// allocated, and every sampling or verify call leaves it zero-filled; a call
+// that fails after using it marks it for a refill.
+//
+// Small calls (a decode step's rows) stage their inputs and outputs through a
+// pinned host mirror of the device part: the inputs are packed there with
+// memcpy and cross in one copy, the outputs come back in one copy.  Larger
+// calls copy from and to the caller's memory directly.
+constexpr size_t STAGE_MAX = (size_t)8 << 20;
+
+struct Arena {
+  int dev = -1;
+  hipStream_t stream = nullptr;
+  char* io = nullptr;          // device part
+  size_t io_cap = 0;
+  char* host = nullptr;        // pinned mirror of io[0, host_cap)
+  size_t host_cap = 0;
+  void* ws = nullptr;
+  size_t ws_cap = 0;
+  bool ws_dirty = false;
 };
+
+static std::mutex g_arena_mu;
+static std::vector<Arena*> g_arena_idle;
+
+// An arena in use: carves the device part into 256-byte-aligned pieces in
+// the order they are taken, and goes back to the idle list when destroyed.
+class ArenaLease {
+ public:
+  ~ArenaLease() {
+    if (!a_) return;
+    std::lock_guard<std::mutex> g(g_arena_mu);
+    g_arena_idle.push_back(a_);
+  }
+  // io_bytes: the sum of the pieces, each rounded up to 256 bytes; the first
+  // stage_bytes of them get a pinned host mirror
+  int acquire(size_t io_bytes, size_t ws_bytes, size_t stage_bytes = 0) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    {
+      std::lock_guard<std::mutex> g(g_arena_mu);
+      for (size_t i = 0; i < g_arena_idle.size(); ++i)
+        if (g_arena_idle[i]->dev == dev) {
+          a_ = g_arena_idle[i];
+          g_arena_idle.erase(g_arena_idle.begin() + i);
+          break;
+        }
+    }
+    if (!a_) {
+      a_ = new Arena;
+      a_->dev = dev;
+      if ((e = hipStreamCreateWithFlags(&a_->stream, hipStreamNonBlocking)) != hipSuccess) {
+        delete a_;
+        a_ = nullptr;
+        return hip_fail(e, "hipStreamCreateWithFlags");
+      }
+    }
+    if (io_bytes > a_->io_cap) {
+      if (a_->io) (void)hipFree(a_->io);
+      a_->io = nullptr;
+      a_->io_cap = 0;
+      if ((e = hipMalloc((void**)&a_->io, io_bytes)) != hipSuccess) return hip_fail(e, "hipMalloc");
+      a_->io_cap = io_bytes;
+    }
+    if (stage_bytes > a_->host_cap) {
+      if (a_->host) (void)hipHostFree(a_->host);
+      a_->host = nullptr;
+      a_->host_cap = 0;
+      if ((e = hipHostMalloc((void**)&a_->host, stage_bytes, hipHostMallocDefault)) != hipSuccess)
+        return hip_fail(e, "hipHostMalloc");
+      a_->host_cap = stage_bytes;
+    }
+    if (ws_bytes > a_->ws_cap) {
+      if (a_->ws) (void)hipFree(a_->ws);
+      a_->ws = nullptr;
+      a_->ws_cap = 0;
+      if ((e = hipMalloc(&a_->ws, ws_bytes)) != hipSuccess) return hip_fail(e, "hipMalloc");
+      a_->ws_cap = ws_bytes;
+      a_->ws_dirty = true;
+    }
+    if (a_->ws_dirty && a_->ws) {
+      if ((e = hipMemsetAsync(a_->ws, 0, a_->ws_cap, a_->stream)) != hipSuccess)
+        return hip_fail(e, "hipMemsetAsync");
+      a_->ws_dirty = false;
+    }
+    return CX_OK;
+  }
+  static size_t piece(size_t n) { return (n + 255) & ~(size_t)255; }
+  char* take(size_t n) {
+    char* p = a_->io + off_;
+    off_ += piece(n);
+    return p;
+  }
+  // the pinned mirror of a device piece
+  char* host(const void* dev_piece) const { return a_->host + ((const char*)dev_piece - a_->io); }
+  void* ws() {
+    a_->ws_dirty = true;              // until finish() says the call left it zero-filled
+    return a_->ws;
+  }
+  size_t ws_cap() const { return a_->ws_cap; }
+  hipStream_t stream() const { return a_->stream; }
+  // the call completed: its kernels left the workspace zero-filled
+  void finish() { a_->ws_dirty = false; }
+
+ private:
+  Arena* a_ = nullptr;
+  size_t off_ = 0;
+};
+
+static hipError_t h2d(void* dst, const void* src, size_t n, hipStream_t s) {
+  return hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, s);
+}
+static hipError_t d2h(void* dst, const void* src, size_t n, hipStream_t s) {
+  return hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, s);
+}
 
 // ------------------------------------------------------------ static scratch
 // The workspace of cx_sample_f32_noalloc: a file-scope device array (each
@@ -365,36 +482,62 @@ int cx_sample_host(const void* logits, int32_t dtype, int64_t ld, int32_t B, int
   if (dtype < 0 || dtype > 2) return fail(CX_EINVAL, "dtype must be 0 (fp32), 1 (bf16) or 2 (fp64)");
   if (B < 0 || V < 1 || ld < V || ldh < 0) return fail(CX_EINVAL, "bad shape");
   if (B == 0) return CX_OK;
+  if (!logits || !prm || !u || !out_id || !row_status) return fail(CX_EINVAL, "null pointer argument");
+  if (ldh > 0 && (!hist || !hist_len)) return fail(CX_EINVAL, "history pointers are null");
+  using AL = ArenaLease;
   const size_t esz = dtype == 2 ? 8 : (dtype == 1 ? 2 : 4);
-  DevBuf dl, dh, dhl, dp, du, did, dst, dpr, dws;
+  const size_t nl = (size_t)B * ld * esz, np = sizeof(cx_row_params) * B, nu = 8 * (size_t)B,
+               nb = 4 * (size_t)B, nh = ldh > 0 ? (size_t)B * ldh * 4 : 0,
+               nhl = ldh > 0 ? nb : 0, npr = out_probs ? (size_t)B * V * 4 : 0;
+  // device pieces: the inputs, then ids and status (staged), then probs
+  const size_t in_bytes = AL::piece(nl) + AL::piece(np) + AL::piece(nu) + AL::piece(nh) +
+                          AL::piece(nhl);
+  const size_t staged = in_bytes + 2 * AL::piece(nb);
+  const bool stage = staged <= STAGE_MAX;
+  ArenaLease L;
+  if (int rc = L.acquire(staged + AL::piece(npr), cx_sample_workspace_bytes(B, V, ldh),
+                         stage ? staged : 0))
+    return rc;
+  char* dl = L.take(nl);
+  char* dp = L.take(np);
+  char* du = L.take(nu);
+  char* dh = L.take(nh);
+  char* dhl = L.take(nhl);
+  char* did = L.take(nb);
+  char* dst = L.take(nb);
+  char* dpr = out_probs ? L.take(npr) : nullptr;
+  const hipStream_t s = L.stream();
   hipError_t e;
-  const size_t ws = cx_sample_workspace_bytes(B, V, ldh);
-  if ((e = dl.alloc((size_t)B * ld * esz)) || (e = dp.alloc(sizeof(cx_row_params) * B)) ||
-      (e = du.alloc(8 * (size_t)B)) || (e = did.alloc(4 * (size_t)B)) ||
-      (e = dst.alloc(4 * (size_t)B)) || (e = dws.alloc(ws)))
-    return hip_fail(e, "hipMalloc");
-  if (ldh > 0 && ((e = dh.alloc((size_t)B * ldh * 4)) || (e = dhl.alloc(4 * (size_t)B))))
-    return hip_fail(e, "hipMalloc");
-  if (out_probs && (e = dpr.alloc((size_t)B * V * 4))) return hip_fail(e, "hipMalloc");
-  if ((e = hipMemcpy(dl.p, logits, (size_t)B * ld * esz, hipMemcpyHostToDevice)) ||
-      (e = hipMemcpy(dp.p, prm, sizeof(cx_row_params) * B, hipMemcpyHostToDevice)) ||
-      (e = hipMemcpy(du.p, u, 8 * (size_t)B, hipMemcpyHostToDevice)) ||
-      (e = hipMemset(dws.p, 0, ws)))
-    return hip_fail(e, "hipMemcpy");
-  if (ldh > 0 && ((e = hipMemcpy(dh.p, hist, (size_t)B * ldh * 4, hipMemcpyHostToDevice)) ||
-                  (e = hipMemcpy(dhl.p, hist_len, 4 * (size_t)B, hipMemcpyHostToDevice))))
-    return hip_fail(e, "hipMemcpy");
-  int rc = sample_impl(dl.p, dtype, ld, B, V, (const int32_t*)dh.p, (const int32_t*)dhl.p, ldh,
-                       (const cx_row_params*)dp.p, (const double*)du.p, (int32_t*)did.p,
-                       (int32_t*)dst.p, out_probs ? (float*)dpr.p : nullptr, dws.p, ws, nullptr);
+  if (stage) {
+    memcpy(L.host(dl), logits, nl);
+    memcpy(L.host(dp), prm, np);
+    memcpy(L.host(du), u, nu);
+    if (ldh > 0) {
+      memcpy(L.host(dh), hist, nh);
+      memcpy(L.host(dhl), hist_len, nhl);
+    }
+    if ((e = h2d(dl, L.host(dl), in_bytes, s))) return hip_fail(e, "hipMemcpyAsync");
+  } else if ((e = h2d(dl, logits, nl, s)) || (e = h2d(dp, prm, np, s)) || (e = h2d(du, u, nu, s)) ||
+             (ldh > 0 && ((e = h2d(dh, hist, nh, s)) || (e = h2d(dhl, hist_len, nhl, s))))) {
+    return hip_fail(e, "hipMemcpyAsync");
+  }
+  int rc = sample_impl(dl, dtype, ld, B, V, ldh > 0 ? (const int32_t*)dh : nullptr,
+                       ldh > 0 ? (const int32_t*)dhl : nullptr, ldh, (const cx_row_params*)dp,
+                       (const double*)du, (int32_t*)did, (int32_t*)dst, (float*)dpr, L.ws(),
+                       L.ws_cap(), s);
   if (rc != CX_OK) return rc;
-  if ((e = hipDeviceSynchronize())) return hip_fail(e, "sample kernel");
-  if ((e = hipMemcpy(out_id, did.p, 4 * (size_t)B, hipMemcpyDeviceToHost)) ||
-      (e = hipMemcpy(row_status, dst.p, 4 * (size_t)B, hipMemcpyDeviceToHost)))
-    return hip_fail(e, "hipMemcpy");
-  if (out_probs &&
-      (e = hipMemcpy(out_probs, dpr.p, (size_t)B * V * 4, hipMemcpyDeviceToHost)))
-    return hip_fail(e, "hipMemcpy");
+  if (stage) {
+    if ((e = d2h(L.host(did), did, 2 * AL::piece(nb), s))) return hip_fail(e, "hipMemcpyAsync");
+  } else if ((e = d2h(out_id, did, nb, s)) || (e = d2h(row_status, dst, nb, s))) {
+    return hip_fail(e, "hipMemcpyAsync");
+  }
+  if (out_probs && (e = d2h(out_probs, dpr, npr, s))) return hip_fail(e, "hipMemcpyAsync");
+  if ((e = hipStreamSynchronize(s))) return hip_fail(e, "sample kernels");
+  L.finish();
+  if (stage) {
+    memcpy(out_id, L.host(did), nb);
+    memcpy(row_status, L.host(dst), nb);
+  }
   return CX_OK;
 }
 
@@ -424,27 +567,32 @@ static int rowop_host(bool trunc, const void* x, int32_t dtype, int64_t ld, int3
   if (!x || !prm || !out || !row_status) return fail(CX_EINVAL, "null pointer argument");
   if (ldh > 0 && (!hist || !hist_len)) return fail(CX_EINVAL, "history pointers are null");
   const size_t esz = dtype == 2 ? 8 : (dtype == 1 ? 2 : 4);
-  DevBuf dx, dh, dhl, dp, dout, dst;
+  const size_t nx = (size_t)B * ld * esz, np = sizeof(cx_row_params) * B,
+               no = (size_t)B * V * 8, nb = 4 * (size_t)B, nh = ldh > 0 ? (size_t)B * ldh * 4 : 0,
+               nhl = ldh > 0 ? nb : 0;
+  using AL = ArenaLease;
+  ArenaLease L;
+  if (int rc = L.acquire(AL::piece(nx) + AL::piece(np) + AL::piece(no) + AL::piece(nb) +
+                             AL::piece(nh) + AL::piece(nhl), 0))
+    return rc;
+  char* dx = L.take(nx);
+  char* dp = L.take(np);
+  char* dout = L.take(no);
+  char* dst = L.take(nb);
+  char* dh = ldh > 0 ? L.take(nh) : nullptr;
+  char* dhl = ldh > 0 ? L.take(nhl) : nullptr;
+  const hipStream_t s = L.stream();
   hipError_t e;
-  if ((e = dx.alloc((size_t)B * ld * esz)) || (e = dp.alloc(sizeof(cx_row_params) * B)) ||
-      (e = dout.alloc((size_t)B * V * 8)) || (e = dst.alloc(4 * (size_t)B)))
-    return hip_fail(e, "hipMalloc");
-  if (ldh > 0 && ((e = dh.alloc((size_t)B * ldh * 4)) || (e = dhl.alloc(4 * (size_t)B))))
-    return hip_fail(e, "hipMalloc");
-  if ((e = hipMemcpy(dx.p, x, (size_t)B * ld * esz, hipMemcpyHostToDevice)) ||
-      (e = hipMemcpy(dp.p, prm, sizeof(cx_row_params) * B, hipMemcpyHostToDevice)))
-    return hip_fail(e, "hipMemcpy");
-  if (ldh > 0 && ((e = hipMemcpy(dh.p, hist, (size_t)B * ldh * 4, hipMemcpyHostToDevice)) ||
-                  (e = hipMemcpy(dhl.p, hist_len, 4 * (size_t)B, hipMemcpyHostToDevice))))
-    return hip_fail(e, "hipMemcpy");
-  int rc = rowop_impl(trunc, dx.p, dtype, ld, B, V, (const int32_t*)dh.p, (const int32_t*)dhl.p,
-                      ldh, (const cx_row_params*)dp.p, (double*)dout.p, V, (int32_t*)dst.p,
-                      nullptr);
+  if ((e = h2d(dx, x, nx, s)) || (e = h2d(dp, prm, np, s)) ||
+      (ldh > 0 && ((e = h2d(dh, hist, nh, s)) || (e = h2d(dhl, hist_len, nhl, s)))))
+    return hip_fail(e, "hipMemcpyAsync");
+  int rc = rowop_impl(trunc, dx, dtype, ld, B, V, (const int32_t*)dh, (const int32_t*)dhl, ldh,
+                      (const cx_row_params*)dp, (double*)dout, V, (int32_t*)dst, s);
   if (rc != CX_OK) return rc;
-  if ((e = hipDeviceSynchronize())) return hip_fail(e, trunc ? "truncate kernel" : "penalties kernel");
-  if ((e = hipMemcpy(out, dout.p, (size_t)B * V * 8, hipMemcpyDeviceToHost)) ||
-      (e = hipMemcpy(row_status, dst.p, 4 * (size_t)B, hipMemcpyDeviceToHost)))
-    return hip_fail(e, "hipMemcpy");
+  if ((e = d2h(out, dout, no, s)) || (e = d2h(row_status, dst, nb, s)))
+    return hip_fail(e, "hipMemcpyAsync");
+  if ((e = hipStreamSynchronize(s))) return hip_fail(e, trunc ? "truncate kernel" : "penalties kernel");
+  L.finish();
   return CX_OK;
 }
 
@@ -481,37 +629,45 @@ int cx_spec_verify_host(const float* target, const float* draft, const int32_t* 
   g_err.clear();
   if (B < 0 || gamma < 1 || V < 1) return fail(CX_EINVAL, "bad shape");
   if (B == 0) return CX_OK;
+  if (!target || !draft_ids || !u || !temperature || !accepted || !next_tok || !used ||
+      !row_status)
+    return fail(CX_EINVAL, "null pointer argument");
   bool any_stoch = false;
   for (int b = 0; b < B; ++b) any_stoch |= temperature[b] != 0.0f;
-  DevBuf dt, dd, di, du, dT, da, dn, dus, dst, dws;
+  if (any_stoch && !draft) return fail(CX_EINVAL, "draft logits are null with a stochastic row");
+  const size_t nt = (size_t)B * (gamma + 1) * V * 4, nd = any_stoch ? (size_t)B * gamma * V * 4 : 0,
+               ni = (size_t)B * gamma * 4, nu = (size_t)B * (gamma + 1) * 8, nb = (size_t)B * 4;
+  using AL = ArenaLease;
+  ArenaLease L;
+  if (int rc = L.acquire(AL::piece(nt) + AL::piece(nd) + AL::piece(ni) + AL::piece(nu) +
+                             5 * AL::piece(nb),
+                         cx_spec_verify_workspace_bytes(B, gamma, V)))
+    return rc;
+  char* dt = L.take(nt);
+  char* dd = any_stoch ? L.take(nd) : nullptr;
+  char* di = L.take(ni);
+  char* du = L.take(nu);
+  char* dT = L.take(nb);
+  char* da = L.take(nb);
+  char* dn = L.take(nb);
+  char* dus = L.take(nb);
+  char* dst = L.take(nb);
+  const hipStream_t s = L.stream();
   hipError_t e;
-  const size_t nt = (size_t)B * (gamma + 1) * V, nd = (size_t)B * gamma * V;
-  const size_t ws = cx_spec_verify_workspace_bytes(B, gamma, V);
-  if ((e = dt.alloc(nt * 4)) || (e = di.alloc((size_t)B * gamma * 4)) ||
-      (e = du.alloc((size_t)B * (gamma + 1) * 8)) || (e = dT.alloc((size_t)B * 4)) ||
-      (e = da.alloc((size_t)B * 4)) || (e = dn.alloc((size_t)B * 4)) ||
-      (e = dus.alloc((size_t)B * 4)) || (e = dst.alloc((size_t)B * 4)) || (e = dws.alloc(ws)))
-    return hip_fail(e, "hipMalloc");
-  if (any_stoch && (e = dd.alloc(nd * 4))) return hip_fail(e, "hipMalloc");
-  if ((e = hipMemcpy(dt.p, target, nt * 4, hipMemcpyHostToDevice)) ||
-      (e = hipMemcpy(di.p, draft_ids, (size_t)B * gamma * 4, hipMemcpyHostToDevice)) ||
-      (e = hipMemcpy(du.p, u, (size_t)B * (gamma + 1) * 8, hipMemcpyHostToDevice)) ||
-      (e = hipMemcpy(dT.p, temperature, (size_t)B * 4, hipMemcpyHostToDevice)) ||
-      (e = hipMemset(dws.p, 0, ws)))
-    return hip_fail(e, "hipMemcpy");
-  if (any_stoch && (e = hipMemcpy(dd.p, draft, nd * 4, hipMemcpyHostToDevice)))
-    return hip_fail(e, "hipMemcpy");
-  int rc = verify_impl((const float*)dt.p, (const float*)dd.p, (const int32_t*)di.p,
-                       (const double*)du.p, (const float*)dT.p, B, gamma, V, (int32_t*)da.p,
-                       (int32_t*)dn.p, (int32_t*)dus.p, (int32_t*)dst.p, dws.p, ws, nullptr,
+  if ((e = h2d(dt, target, nt, s)) || (e = h2d(di, draft_ids, ni, s)) ||
+      (e = h2d(du, u, nu, s)) || (e = h2d(dT, temperature, nb, s)) ||
+      (any_stoch && (e = h2d(dd, draft, nd, s))))
+    return hip_fail(e, "hipMemcpyAsync");
+  int rc = verify_impl((const float*)dt, (const float*)dd, (const int32_t*)di,
+                       (const double*)du, (const float*)dT, B, gamma, V, (int32_t*)da,
+                       (int32_t*)dn, (int32_t*)dus, (int32_t*)dst, L.ws(), L.ws_cap(), s,
                        any_stoch);
   if (rc != CX_OK) return rc;
-  if ((e = hipDeviceSynchronize())) return hip_fail(e, "verify kernels");
-  if ((e = hipMemcpy(accepted, da.p, (size_t)B * 4, hipMemcpyDeviceToHost)) ||
-      (e = hipMemcpy(next_tok, dn.p, (size_t)B * 4, hipMemcpyDeviceToHost)) ||
-      (e = hipMemcpy(used, dus.p, (size_t)B * 4, hipMemcpyDeviceToHost)) ||
-      (e = hipMemcpy(row_status, dst.p, (size_t)B * 4, hipMemcpyDeviceToHost)))
-    return hip_fail(e, "hipMemcpy");
+  if ((e = d2h(accepted, da, nb, s)) || (e = d2h(next_tok, dn, nb, s)) ||
+      (e = d2h(used, dus, nb, s)) || (e = d2h(row_status, dst, nb, s)))
+    return hip_fail(e, "hipMemcpyAsync");
+  if ((e = hipStreamSynchronize(s))) return hip_fail(e, "verify kernels");
+  L.finish();
   return CX_OK;
 }
 

@@ -76,17 +76,21 @@ class Sampler:
         if not generated_ids or (rp == 1.0 and pres == 0.0 and freq == 0.0):
             return None
         n_keep = int(getattr(params, "n_keep", 0))
-        win = list(generated_ids[-max(64, n_keep):]) if n_keep else list(generated_ids)
-        try:
-            h = np.asarray(win, dtype=np.int64)
-        except OverflowError:
-            h = np.asarray([t if -1 <= t < 2**62 else -1 for t in win], dtype=np.int64)
-        inr = (h >= 0) & (h < self.vocab_size)
-        if rp != 1.0 and np.any(inr & (h >= V)):
-            # the reference indexes the row with every in-range id
-            bad = int(h[inr & (h >= V)][0])
-            raise IndexError(f"index {bad} is out of bounds for axis 0 with size {V}")
-        h = np.where(inr & (h < V), h, -1)
+        seq = generated_ids[-max(64, n_keep):] if n_keep else generated_ids
+        if isinstance(seq, np.ndarray):
+            h = seq.astype(np.int64)
+        else:
+            try:
+                h = np.fromiter(seq, dtype=np.int64, count=len(seq))
+            except OverflowError:
+                h = np.asarray([t if -1 <= t < 2**62 else -1 for t in seq], dtype=np.int64)
+        if rp != 1.0 and V < self.vocab_size:
+            bad = (h >= V) & (h < self.vocab_size)
+            if bad.any():
+                # the reference indexes the row with every in-range id
+                raise IndexError(f"index {int(h[bad][0])} is out of bounds for axis 0 "
+                                 f"with size {V}")
+        h = np.where((h >= 0) & (h < min(V, self.vocab_size)), h, -1)
         if h.size > WINDOW_MAX:
             if freq != 0.0:
                 raise ValueError(f"frequency penalty over a window of {h.size} ids: the "
@@ -153,6 +157,7 @@ class Sampler:
         """
         on_dev = _is_torch_cuda(logits)
         if on_dev:
+            import torch
             B, V = int(logits.shape[0]), int(logits.shape[1])
         else:
             x = np.asarray(logits)
@@ -184,10 +189,16 @@ class Sampler:
         stoch = [float(p.temperature) != 0.0 for p in plist]
         seeds = [getattr(p, "seed", None) for p in plist]
 
-        def run(u):
+        def run(u, rows=None):
+            """Sample every row, or the listed rows only (returned in that order)."""
+            sel = slice(None) if rows is None else rows
+            h = None if hist is None else hist[sel]
+            hl = None if hist_len is None else hist_len[sel]
             if on_dev:
-                return self._run_device(logits, prm, u, hist, hist_len)
-            ids, st, _ = _lib.sample_host(x, prm, hist, hist_len, u)
+                xs = logits if rows is None else logits.index_select(
+                    0, torch.as_tensor(rows, device=logits.device))
+                return self._run_device(xs, prm[sel], u[sel], h, hl)
+            ids, st, _ = _lib.sample_host(x if rows is None else x[rows], prm[sel], h, hl, u[sel])
             return ids, st
 
         with self._lock:
@@ -197,10 +208,16 @@ class Sampler:
             draws = [(int(s) & 0xFF) == _lib.ROW_OK for s in st]
             if any(stoch[b] and seeds[b] is None and not draws[b] for b in range(B)):
                 # a row that draws nothing must not take a variate from the
-                # shared generator: hand the variates to the drawing rows only
+                # shared generator: the variates go to the drawing rows only,
+                # and the rows whose variate moved are sampled again (whether
+                # a row draws does not depend on its variate)
                 self._rng.bit_generator.state = state
-                u = self._uniforms(stoch, seeds, draws)
-                ids, st = run(u)
+                u2 = self._uniforms(stoch, seeds, draws)
+                redo = [b for b in range(B) if draws[b] and u2[b] != u[b]]
+                if redo:
+                    ids = np.array(ids)
+                    st = np.array(st)
+                    ids[redo], st[redo] = run(u2, redo)
             out = []
             self._rng.bit_generator.state = state
             for b in range(B):

@@ -216,8 +216,13 @@ def test_unseeded_generator_advances_like_the_reference():
     assert s._rng.bit_generator.state == shadow.bit_generator.state
 
 
-def test_sample_batch_equals_sequential_calls():
-    _say("[gpu] Sampler.sample_batch vs sequential sample")
+@pytest.mark.parametrize("on_device", [False, True])
+def test_sample_batch_equals_sequential_calls(on_device):
+    """Row 9 falls back to argmax without a draw, so the unseeded rows after
+    it take the shared generator's variates one place earlier than the first
+    launch gave them, and are sampled again."""
+    import torch
+    _say(f"[gpu] Sampler.sample_batch vs sequential sample (device tensor: {on_device})")
     V = 500
     rng = np.random.default_rng(11)
     X = rng.normal(0, 2, (24, V)).astype(np.float32)
@@ -235,7 +240,7 @@ def test_sample_batch_equals_sequential_calls():
     seq = [a.sample(X[b], params[b], hists[b]) for b in range(24)]
     b_ = Sampler(V)
     b_._rng = np.random.default_rng(99)
-    bat = b_.sample_batch(X, params, hists)
+    bat = b_.sample_batch(torch.from_numpy(X).cuda() if on_device else X, params, hists)
     assert bat == seq
     assert a._rng.bit_generator.state == b_._rng.bit_generator.state
 
