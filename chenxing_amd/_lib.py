@@ -19,7 +19,7 @@ LIB_PATH = os.path.join(HERE, "libcx_sampler.so")
 
 CX_OK, CX_EINVAL, CX_EHIP, CX_ENOSPACE = 0, -1, -2, -3
 ROW_OK, ROW_GREEDY, ROW_ARGMAX, ROW_ERROR, ROW_UNSUPPORTED = 0, 1, 2, 3, 4
-FLAG_SLOW, FLAG_EXACT = 0x100, 0x200
+FLAG_SLOW, FLAG_EXACT, FLAG_DEEP = 0x100, 0x200, 0x400
 
 _lib = None
 _lock = threading.Lock()

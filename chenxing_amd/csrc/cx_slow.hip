@@ -8,11 +8,15 @@
 //                     exactly in fp64 and the region finished again; pending
 //                     rows (or, for fp64 logits, every row) get the exact
 //                     multi-pass path, as does any row the steps before
-//                     cannot decide.  A workgroup whose row is decided reads
-//                     its status word and exits.
+//                     cannot decide; a pending top-p / min-p row without
+//                     top-k, typical-p or penalties first tries the
+//                     three-pass deep-nucleus path (cx_deep.hpp).  A
+//                     workgroup whose row is decided reads its status word
+//                     and exits.
 //   penalties_kernel  Sampler.apply_penalties, grid (rows, chunks of PEN_CHUNK)
 //   truncate_kernel   Sampler._truncate, one workgroup per row
 #include "cx_slow.hpp"
+#include "cx_deep.hpp"
 #include "cx_finish.hpp"
 #include "cx_timing.hpp"
 
@@ -70,6 +74,8 @@ __global__ __launch_bounds__(WG) void slow_kernel(SampleArgs A) {
   }
   if (state == REFINE && refine_row(A, row, dyn, red_d, red_i)) return;
   __syncthreads();
+  if (deep_row(A, row, dyn, red_d, red_i)) return;
+  __syncthreads();
   slow_row(A, row, dyn, red_d, red_i);
 }
 
@@ -101,7 +107,9 @@ static int set_lds(K kernel, int bytes, int& attr) {
 
 int launch_slow(const SampleArgs& A, hipStream_t s) {
   static int attr = 0;
-  // the multi-pass layout, or a refined row's finisher region
+  // the multi-pass layout, or a refined row's finisher region (which also
+  // holds the deep-nucleus path's tables)
+  static_assert(DEEP_LDS <= FIN_CAP * 32, "deep-nucleus LDS");
   const int bytes = max(A.slow_lds_bytes, FIN_CAP * 32);
   if (int e = set_lds(slow_kernel, bytes, attr)) return e;
   timed_launch(CX_KERNEL_SAMPLE_SLOW, slow_kernel, dim3(A.B), dim3(WG), bytes, s, A);

@@ -39,6 +39,7 @@ extern "C" {
 #define CX_ROW_UNSUPPORTED 4  /* input outside the library's limits (history window) */
 /* row_status high bits: how the row was computed (informational) */
 #define CX_ROW_FLAG_SLOW   0x100  /* resolved by the exact multi-pass row path */
+#define CX_ROW_FLAG_DEEP   0x400  /* with CX_ROW_FLAG_SLOW: by its three-pass deep-nucleus variant */
 #define CX_ROW_FLAG_EXACT  0x200  /* normaliser recomputed in fp64 for a near-threshold decision */
 
 /* Per-row sampling parameters, 64 bytes.  Mirrors SamplingParams

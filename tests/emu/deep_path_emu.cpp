@@ -1,0 +1,83 @@
+// Runs the deep-nucleus row path (deep_row, cx_deep.hpp) on the host, one
+// workgroup at a time, with every buffer an exact-size heap allocation under
+// AddressSanitizer.  Each row's maximum goes into its slice record, as the
+// fused kernel leaves it.  Output per row: the sampled id, or -2 where the
+// path hands the row to the multi-pass path.
+// usage: deep_path_emu IN OUT (written and read by tests/test_emu_deep_path.py)
+#include "cx_deep.hpp"
+thread_local EmuDim threadIdx;
+EmuDim blockIdx;
+emu::Wave* emu::waves;
+std::barrier<>* emu::block_bar;
+using namespace cx;
+
+template <class T> static T* rd(FILE* f, size_t n) {
+  T* p = (T*)malloc(n * sizeof(T) > 0 ? n * sizeof(T) : 1);
+  if (n && fread(p, sizeof(T), n, f) != n) { fprintf(stderr, "short read\n"); exit(2); }
+  return p;
+}
+
+int main(int argc, char** argv) {
+  FILE* in = fopen(argv[1], "rb");
+  FILE* out = fopen(argv[2], "wb");
+  int32_t ngroups;
+  if (fread(&ngroups, 4, 1, in) != 1) return 2;
+  for (int g = 0; g < ngroups; ++g) {
+    int32_t hdr[3];
+    if (fread(hdr, 4, 3, in) != 3) return 2;
+    const int B = hdr[0], V = hdr[1], bf16 = hdr[2];
+    const size_t esz = bf16 ? 2 : 4;
+    void* x = rd<unsigned char>(in, (size_t)B * V * esz);
+    cx_row_params* prm = rd<cx_row_params>(in, B);
+    double* u = rd<double>(in, B);
+    int32_t* ids = (int32_t*)malloc(4 * B);
+    int32_t* st = (int32_t*)malloc(4 * B);
+    SplitStats* stats = (SplitStats*)calloc(B, sizeof(SplitStats));
+    for (int b = 0; b < B; ++b) {
+      double m = -INFINITY;
+      for (int i = 0; i < V; ++i) {
+        const double v = bf16 ? (double)__uint_as_float((uint32_t)((const uint16_t*)x)[(size_t)b * V + i] << 16)
+                              : (double)((const float*)x)[(size_t)b * V + i];
+        if (v > m) m = v;                       // NaN never wins, as in the fused kernel
+      }
+      stats[b].m = m;
+    }
+    SampleArgs A;
+    memset(&A, 0, sizeof A);
+    A.logits = x; A.ld = V; A.B = B; A.V = V; A.ldh = 0;
+    A.prm = prm; A.u = u; A.out_id = ids; A.row_status = st; A.out_probs = nullptr;
+    A.nsplit = 1; A.stats = stats; A.bf16 = bf16; A.logV = log((double)V);
+    A.vec_ok = ((uintptr_t)x % 16 == 0) && ((size_t)V * esz % 16 == 0);   // as the library sets it
+    for (int row = 0; row < B; ++row) {
+      unsigned char* dyn = (unsigned char*)malloc(DEEP_LDS);
+      for (size_t i = 0; i < (size_t)DEEP_LDS; ++i) dyn[i] = (unsigned char)(i * 131 + 7);
+      emu::Wave waves[16];
+      emu::waves = waves;
+      std::barrier<> bb(1024);
+      emu::block_bar = &bb;
+      blockIdx.x = row;
+      int decided = -1;
+      std::vector<std::thread> th;
+      th.reserve(1024);
+      for (int t = 0; t < 1024; ++t)
+        th.emplace_back([&, t] {
+          threadIdx.x = t;
+          __shared__ double red_d[2 * NWAVE + 4];
+          __shared__ int red_i[2 * NWAVE + 4];
+          const bool r = deep_row(A, row, dyn, red_d, red_i);
+          if (t == 0) decided = r ? 1 : 0;
+          waves[t >> 6].bar.arrive_and_drop();
+          bb.arrive_and_drop();
+        });
+      for (auto& h : th) h.join();
+      free(dyn);
+      if (!decided) { ids[row] = -2; st[row] = -2; }
+    }
+    fwrite(ids, 4, B, out);
+    fwrite(st, 4, B, out);
+    free(x); free(prm); free(u); free(ids); free(st); free(stats);
+    fprintf(stderr, "group V=%d B=%d done\n", V, B);
+  }
+  fclose(out);
+  return 0;
+}

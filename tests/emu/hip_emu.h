@@ -133,6 +133,22 @@ template <class T> inline T atomicCAS(T* p, T cmp, T v) {
   __atomic_compare_exchange_n(p, &cmp, v, false, __ATOMIC_SEQ_CST, __ATOMIC_SEQ_CST);
   return cmp;
 }
+// Raw buffer loads: a descriptor is a base and a byte count; dwords past the
+// count read as zero and touch no memory.
+struct __amdgpu_buffer_rsrc_t { const char* p; int n; };
+inline __amdgpu_buffer_rsrc_t __builtin_amdgcn_make_buffer_rsrc(void* p, short, int n, int) {
+  return {(const char*)p, n};
+}
+typedef uint32_t emu_u32x4 __attribute__((vector_size(16)));
+inline emu_u32x4 __builtin_amdgcn_raw_buffer_load_b128(__amdgpu_buffer_rsrc_t r, int voff, int soff,
+                                                       int) {
+  emu_u32x4 v = {0u, 0u, 0u, 0u};
+  for (int k = 0; k < 4; ++k) {
+    const int o = voff + soff + 4 * k;
+    if (o >= 0 && o + 4 <= r.n) { uint32_t w; std::memcpy(&w, r.p + o, 4); v[k] = w; }
+  }
+  return v;
+}
 typedef void* hipStream_t;
 #include <algorithm>
 using std::min;

@@ -1,0 +1,135 @@
+"""The deep-nucleus row path (cx_deep.hpp ``deep_row``) compiled for the host
+and run under AddressSanitizer: one OS thread per work-item, a std::barrier
+per workgroup for __syncthreads, per-wave exchanges for ballots and
+shuffles (tests/emu/hip_emu.h).  Every LDS and global buffer is an
+exact-size heap allocation, so an out-of-bounds access fails the run.  On
+top-p / min-p rows with deep nuclei (fp32 rows of odd length, so most rows
+start unaligned, and bf16 rows full of ties) every row the path decides must
+sample the oracle's id; a row it hands back (-2) is allowed only where the
+test expects it (NaN).  CPU only."""
+from __future__ import annotations
+
+import os
+import re
+import shutil
+import struct
+import subprocess
+import tempfile
+
+import numpy as np
+import pytest
+
+from chenxing_amd.params import RowParams, pack_rows
+from chenxing_amd import workloads as W
+from chenxing_amd.workloads import bf16_to_f32, f32_to_bf16_rne
+from oracle import sampler_ref as R
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+CSRC = os.path.join(ROOT, "chenxing_amd", "csrc")
+
+pytestmark = pytest.mark.skipif(shutil.which("g++") is None, reason="needs g++")
+
+
+def _build(tmp: str) -> str:
+    src = os.path.join(tmp, "src")
+    os.makedirs(os.path.join(tmp, "inc", "hip"))
+    os.makedirs(src)
+    shutil.copy(os.path.join(HERE, "emu", "hip_emu.h"), os.path.join(tmp, "inc", "hip", "hip_runtime.h"))
+    for f in ("cx_device.hpp", "cx_deep.hpp", "cx_internal.hpp"):
+        text = open(os.path.join(CSRC, f)).read()
+        text = re.sub(r"^#define CX_LDS __attribute__\(\(address_space\(3\)\)\)", "#define CX_LDS",
+                      text, flags=re.M)
+        text = re.sub(r"^#define CX_CONST __attribute__\(\(address_space\(4\)\)\)", "#define CX_CONST",
+                      text, flags=re.M)
+        open(os.path.join(src, f), "w").write(text)
+    shutil.copy(os.path.join(ROOT, "include", "cx_sampler.h"), src)
+    exe = os.path.join(tmp, "deep_path_emu")
+    cmd = ["g++", "-std=c++20", "-O1", "-g", "-fsanitize=address", "-fno-omit-frame-pointer",
+           "-pthread", "-I", os.path.join(tmp, "inc"), "-I", src, "-include", "hip/hip_runtime.h",
+           os.path.join(HERE, "emu", "deep_path_emu.cpp"), "-o", exe]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-3000:]
+    return exe
+
+
+def _groups():
+    rng = np.random.default_rng(5)
+    out = []
+    # fp32, odd V: rows 1.. start unaligned
+    V = 30011
+    x = rng.normal(0, 1.0, (9, V)).astype(np.float32)
+    x[:, rng.choice(V, 4, replace=False)] += np.float32(6.0)
+    prm = [RowParams(temperature=0.7, top_p=0.9), RowParams(temperature=1.0, top_p=0.99),
+           RowParams(temperature=1.3, top_p=0.5), RowParams(temperature=1.0, top_p=0.95, min_p=0.02),
+           RowParams(temperature=0.9, top_p=1.0, min_p=0.001), RowParams(temperature=1.1, top_p=0.0),
+           RowParams(temperature=1.0, top_p=0.999), RowParams(temperature=2.0, top_p=0.8),
+           RowParams(temperature=1.0, top_p=0.9)]
+    x[8, 123] = np.nan                                   # handed back: NaN
+    x[0, rng.choice(V, 100, replace=False)] = -np.inf    # masked tokens
+    out.append(("f32", x, prm, {8}, None))
+    # bf16 with many equal values at the cut
+    V = 40000
+    xb = f32_to_bf16_rne(rng.normal(0, 2.0, (6, V)).astype(np.float32))
+    xb[0, rng.choice(V, 100, replace=False)] = 0xFF80    # -inf: masked tokens
+    prm = [RowParams(temperature=1.5, top_p=0.9), RowParams(temperature=1.0, top_p=0.7),
+           RowParams(temperature=0.8, top_p=0.95, min_p=0.05), RowParams(temperature=1.2, top_p=0.6),
+           RowParams(temperature=1.0, top_p=1.0, min_p=0.3), RowParams(temperature=1.4, top_p=0.97)]
+    out.append(("bf16", xb, prm, set(), None))
+    # rows of the B=1024 V=256000 bf16 heterogeneous workload whose cut
+    # element holds ~5e-7 of the mass: too little for running sums kept to
+    # 2^-42 of the total to place the cut robustly
+    w = W.hetero_bf16()
+    rows = [1, 227, 669, 677, 901]
+    out.append(("bf16", np.ascontiguousarray(w.logits[rows]), [w.params[b] for b in rows], set(),
+                w.u[rows]))
+    return out
+
+
+def _splits_a_tie(row: np.ndarray, prm: RowParams) -> bool:
+    """Whether the top-p cut keeps only part of a group of equal values."""
+    z = (row.astype(np.float64) - row.max()) / prm.temperature
+    p = np.exp(z) / np.exp(z).sum()
+    order = np.argsort(-p, kind="stable")
+    cut = int(np.searchsorted(np.cumsum(p[order]), prm.top_p)) + 1
+    v = p[order[min(cut, p.size) - 1]]
+    return int(np.sum(p[order[:cut]] == v)) < int(np.sum(p == v))
+
+
+def test_deep_path_emulated_on_deep_nucleus_rows():
+    groups = _groups()
+    kind, xb, prm, _, _ = groups[1]
+    assert any(_splits_a_tie(r, q) for r, q in zip(bf16_to_f32(xb), prm) if q.top_p < 1.0)
+    us = []
+    with tempfile.TemporaryDirectory() as tmp:
+        exe = _build(tmp)
+        fin, fout = os.path.join(tmp, "in.bin"), os.path.join(tmp, "out.bin")
+        with open(fin, "wb") as f:
+            f.write(struct.pack("i", len(groups)))
+            for kind, x, prm, _, ug in groups:
+                B, V = x.shape
+                u = ug if ug is not None else np.random.default_rng(B * 7 + V).random(B)
+                us.append(u)
+                f.write(struct.pack("iii", B, V, 1 if kind == "bf16" else 0))
+                for a in (x, pack_rows(prm), u.astype(np.float64)):
+                    f.write(np.ascontiguousarray(a).tobytes())
+        r = subprocess.run([exe, fin, fout], capture_output=True, text=True, timeout=900)
+        assert r.returncode == 0, r.stderr[-4000:]
+        out = open(fout, "rb").read()
+    off = 0
+    decided = 0
+    for (kind, x, prm, back, _), u in zip(groups, us):
+        B, V = x.shape
+        ids = np.frombuffer(out, np.int32, B, off)
+        off += 8 * B
+        rows = bf16_to_f32(x) if kind == "bf16" else x
+        for b in range(B):
+            if b in back:
+                assert ids[b] == -2, (kind, b)
+                continue
+            assert ids[b] != -2, (kind, b, "handed back")
+            res = R.sample_row(rows[b], prm[b], None, u[b], tie="stable")
+            assert res.status == R.STATUS_OK
+            assert int(ids[b]) == res.token, (kind, b, int(ids[b]), res.token)
+            decided += 1
+    assert decided == 19
