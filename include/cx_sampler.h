@@ -191,6 +191,9 @@ int cx_truncate_host(const double* probs, int64_t ld, int32_t B, int32_t V,
  *             (the caller samples row gamma with the full sampler, :171)
  *  used       [B] int32 number of uniforms the reference would have consumed
  *  row_status [B] int32 CX_ROW_* flags
+ *  workspace  device scratch of cx_spec_verify_workspace_bytes(B, gamma, V)
+ *             bytes; any contents (every call writes what it reads).  One
+ *             workspace per stream.
  */
 int cx_spec_verify_f32(const float* target, const float* draft, const int32_t* draft_ids,
                        const double* u, const float* temperature,
