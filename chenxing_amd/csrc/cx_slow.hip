@@ -26,8 +26,9 @@ constexpr int PEN_CHUNK = 16384;     // elements per penalties_kernel workgroup
 
 // A row whose region is complete and whose only open question is a top-p
 // cut within the streamed normaliser's error bound: the exact fp64
-// normaliser over the row, then the region finished with it.  Returns false,
-// with nothing written, if the row still needs the multi-pass path.
+// normaliser over the row (streamed with its loads ahead when the row has no
+// penalty window), then the region finished with it.  Returns false, with
+// nothing written, if the row still needs the multi-pass path.
 __device__ inline bool refine_row(const SampleArgs& A, int row, unsigned char* dyn, double* red_d,
                                   int* red_i) {
   const cx_row_params P = A.prm[row];
@@ -41,7 +42,8 @@ __device__ inline bool refine_row(const SampleArgs& A, int row, unsigned char* d
     M = m > M ? m : M;
   }
   if (!(M > -__builtin_inf()) || !(M < __builtin_inf())) return false;
-  const double S = exact_norm(R, M, 1.0 / P.temperature, red_d);
+  const double S = R.pen || A.f64 ? exact_norm(R, M, 1.0 / P.temperature, red_d)
+                                  : deep_exact_sum(A, row, M, 1.0 / P.temperature, red_d);
   __syncthreads();                       // the penalty tables in dyn are dead from here
   if (!(S > 0.0) || !(S < __builtin_inf())) return false;
   return finish_row_fast<FIN_CAP>(A, row, P, dyn, red_d, red_i, S) == FIN_DONE;
