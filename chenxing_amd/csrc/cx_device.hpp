@@ -168,11 +168,21 @@ __device__ __forceinline__ double wave_scan_dpp(double v) {
   v += dpp_update0<0x143, 0xC>(v);   // row_bcast:31 into rows 2 and 3
   return v;
 }
+__device__ __forceinline__ int wave_scan_dpp(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, true);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, true);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, true);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, true);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, true);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, true);
+  return v;
+}
 
 struct OpAdd { template <typename T> __device__ T operator()(T a, T b) const { return a + b; } };
 struct OpMax { template <typename T> __device__ T operator()(T a, T b) const { return a > b ? a : b; } };
 struct OpMin { template <typename T> __device__ T operator()(T a, T b) const { return a < b ? a : b; } };
-struct OpOr { __device__ int operator()(int a, int b) const { return a | b; } };
+struct OpOr { template <typename T> __device__ T operator()(T a, T b) const { return a | b; } };
+struct OpAnd { template <typename T> __device__ T operator()(T a, T b) const { return a & b; } };
 
 // Block-wide reductions through a small LDS scratch (>= NWAVE slots).
 template <typename T>

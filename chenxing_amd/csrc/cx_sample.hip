@@ -245,6 +245,11 @@ __device__ __noinline__ WState wave_compact_call(CX_LDS uint32_t* wkey, CX_LDS i
                                                  CX_LDS uint32_t* shared) {
   constexpr int PER = CAPW / 64;
   const int l = lane_id();
+  // the arguments are wave-uniform: scalar registers keep the radix loop's
+  // control and prefix off the vector unit
+  n = __builtin_amdgcn_readfirstlane(n);
+  kw = __builtin_amdgcn_readfirstlane(kw);
+  tau = (uint32_t)__builtin_amdgcn_readfirstlane((int)tau);
   uint32_t k[PER];
   int32_t id[PER];
 #pragma unroll
@@ -253,25 +258,27 @@ __device__ __noinline__ WState wave_compact_call(CX_LDS uint32_t* wkey, CX_LDS i
     k[e] = pos < n ? wkey[pos] : 0u;
     id[e] = pos < n ? widx[pos] : 0;
   }
-  // bits every held key shares need no radix step
+  // bits above the highest and below the lowest bit in which held keys
+  // differ need no radix step (a bf16 value's key has 16 zero low bits)
   uint32_t kand = 0xFFFFFFFFu, kor = 0u;
 #pragma unroll
   for (int e = 0; e < PER; ++e)
     if (k[e]) { kand &= k[e]; kor |= k[e]; }
-  for (int o = 32; o > 0; o >>= 1) {
-    kand &= __shfl_xor(kand, o);
-    kor |= __shfl_xor(kor, o);
-  }
+  kand = wave_reduce(kand, OpAnd());
+  kor = wave_reduce(kor, OpOr());
   const uint32_t diff = kand ^ kor;
   const int hb = diff ? 31 - __clz(diff) : -1;
+  const int lb = diff ? __builtin_ctz(diff) : 0;
   uint32_t prefix = hb < 0 ? kand : (hb == 31 ? 0u : (kand & ~((2u << hb) - 1u)));
-  for (int bit = hb; bit >= 0; --bit) {
+  for (int bit = hb; bit >= lb; --bit) {
     uint32_t cand = prefix | (1u << bit);
     int cnt = 0;
 #pragma unroll
     for (int e = 0; e < PER; ++e) cnt += __popcll(ballot(k[e] >= cand));
     if (cnt >= kw) prefix = cand;
   }
+  // the shared low bits: prefix is then the kw-th largest key itself
+  if (hb >= 0) prefix |= kand & ((1u << lb) - 1u);
   if (prefix > tau) tau = prefix;
   int m = 0;
 #pragma unroll
@@ -295,8 +302,9 @@ __device__ __noinline__ WState wave_compact_call(CX_LDS uint32_t* wkey, CX_LDS i
 
 __device__ __forceinline__ void wave_compact(WaveBuf& w, bool share) {
   WState r = wave_compact_call(w.key, w.idx, w.n, w.tau, w.kw, share, w.shared);
-  w.n = r.n;
-  raise_tau(w, r.tau);
+  // uniform results: keep them in scalar registers
+  w.n = __builtin_amdgcn_readfirstlane(r.n);
+  raise_tau(w, (uint32_t)__builtin_amdgcn_readfirstlane((int)r.tau));
 }
 
 // Insert one element slot of the wave (key 0 = not a candidate), compacting
@@ -415,10 +423,15 @@ __device__ __forceinline__ void rescale(float vmax, float c, float lim, SState& 
 }
 
 // Append the candidates of one chunk (some lane of the wave has one: its
-// chunk maximum reaches the threshold).  With room for all 64 x U x NE
-// elements of the flagged lanes, lanes append on their own through the LDS
-// counter; otherwise the element slots go through wave_insert1 one by one.
-// Penalised elements never enter: their penalised values join afterwards.
+// chunk maximum reaches the threshold).  Penalised elements never enter:
+// their penalised values join afterwards.
+//  - Few flagged lanes (room for all their elements): lanes append on their
+//    own through the wave's LDS counter; a slot no lane reaches costs a
+//    compare and a branch.
+//  - Otherwise each lane marks its element slots at or above the threshold
+//    and a wave prefix sum of the marks gives every lane its write offset.
+//    When the marks do not fit, the wave compacts first; if they still do
+//    not fit the element slots go through wave_insert1 one by one.
 template <bool BF16>
 __device__ __forceinline__ void append_chunk(WaveBuf& wb,
                                              const float (&xs)[Elem<BF16>::U][Elem<BF16>::NE],
@@ -427,18 +440,18 @@ __device__ __forceinline__ void append_chunk(WaveBuf& wb,
   using E = Elem<BF16>;
   constexpr int NE = E::NE;
   constexpr int U = E::U;
+  static_assert(U * NE <= 32, "a lane's element slots in one mask word");
   const int lanes = __popcll(ballot(flagged));
   if (wb.n + lanes * U * NE <= CAPW) {
     if (flagged) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const float (&x)[NE] = xs[u];
         const int vi = vb + u * 64;
         const int e0 = vi * NE + lo;
 #pragma unroll
         for (int j = 0; j < NE; ++j) {
-          if (vi < nv && x[j] >= wb.tauf && !(pen_on && pen_bit(X, e0 + j - lo))) {
-            const uint32_t k = f2key(x[j]);
+          if (vi < nv && xs[u][j] >= wb.tauf && !(pen_on && pen_bit(X, e0 + j - lo))) {
+            const uint32_t k = f2key(xs[u][j]);
             const int pos = __hip_atomic_fetch_add(wb.cnt, 1, CX_RELAXED_WG);
             wb.key[pos] = k;
             wb.idx[pos] = e0 + j;
@@ -448,6 +461,62 @@ __device__ __forceinline__ void append_chunk(WaveBuf& wb,
       }
     }
     wb.n = lds_load(wb.cnt);
+    return;
+  }
+  // this lane's element slots at or above the threshold, unpenalised (the
+  // chunk's penalty words are read together: one LDS round trip)
+  auto select = [&]() {
+    uint32_t m = 0u;
+    if (flagged) {
+      uint32_t pw[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int vi = vb + u * 64;
+        pw[u] = pen_on ? X.bitmap[vi < nv ? (vi * NE) >> 5 : 0] : 0u;
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int vi = vb + u * 64;
+        const uint32_t pb = pw[u] >> ((vi * NE) & 31);
+#pragma unroll
+        for (int j = 0; j < NE; ++j)
+          if (vi < nv && xs[u][j] >= wb.tauf && !((pb >> j) & 1u)) m |= 1u << (u * NE + j);
+      }
+    }
+    return m;
+  };
+  uint32_t m = select();
+  int c = __popc(m);
+  int incl = wave_scan_dpp(c);
+  int total = __builtin_amdgcn_readlane(incl, 63);
+  if (wb.n + total > CAPW && wb.n > wb.kw) {
+    // make room first: keep the kw largest held, raising the threshold
+    wave_compact(wb, share);
+    m = select();
+    c = __popc(m);
+    incl = wave_scan_dpp(c);
+    total = __builtin_amdgcn_readlane(incl, 63);
+  }
+  if (wb.n + total <= CAPW) {
+    // each lane writes its slots at its offset in the wave's prefix sum
+    const int base = wb.n + incl - c;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int e0 = (vb + u * 64) * NE + lo;
+#pragma unroll
+      for (int j = 0; j < NE; ++j) {
+        const int s = u * NE + j;
+        if ((m >> s) & 1u) {
+          const int pos = base + __popc(m & ((1u << s) - 1u));
+          const uint32_t k = f2key(xs[u][j]);
+          wb.key[pos] = k;
+          wb.idx[pos] = e0 + j;
+          ck = k > ck ? k : ck;
+        }
+      }
+    }
+    wb.n += total;
+    if (lane_id() == 0) *wb.cnt = wb.n;
   } else {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -517,6 +586,11 @@ __device__ __forceinline__ void stream_stoch(__amdgpu_buffer_rsrc_t rs,
 #pragma unroll
       for (int j = 0; j < NE; ++j) ts += __builtin_amdgcn_exp2f(__builtin_fmaf(x[u][j], c, st.nR));
     st.s += (double)ts;
+    // The sum is taken here, before the refill below.  Left free, the
+    // compiler sinks it past the refill, the refill then needs registers
+    // other than the buffer's, and the loop's back edge copies them over
+    // after waiting for every load in flight.
+    __asm__ volatile("" : "+v"(st.s));
     const bool flagged = cmax >= wb.tauf;
     if (ballot(flagged)) {
       append_chunk<BF16>(wb, x, flagged, vb, nv, lo, pen_on, X, share, ck);
@@ -558,7 +632,6 @@ __device__ __forceinline__ void stream_scalar(const char* rowp, int s0, int lo, 
     uint32_t k = 0u;
     if (valid && x >= wb.tauf && !(pen_on && pen_bit(X, e - lo))) k = f2key(x);
     if (ballot(k != 0u)) {
-      wb.n = lds_load(wb.cnt);
       if (wave_insert1(wb, k, e, share)) ck = k > ck ? k : ck;
       if (lane_id() == 0) *wb.cnt = wb.n;
     }
@@ -1023,8 +1096,8 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   WaveBuf wb;
   wb.key = to_lds((uint32_t*)(dyn + A.off_wkey) + wave_id() * CAPW);
   wb.idx = to_lds((int32_t*)(dyn + A.off_widx) + wave_id() * CAPW);
-  wb.cnt = to_lds(&w_cnt[wave_id()]);
   wb.shared = to_lds(&s_shared);
+  wb.cnt = to_lds(&w_cnt[wave_id()]);
   wb.n = 0;
   wb.tau = 1u;
   wb.tauf = -__builtin_inff();
