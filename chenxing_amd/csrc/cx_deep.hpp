@@ -220,8 +220,8 @@ __device__ __forceinline__ void deep_stream(const DeepRow& R, int lo, int stride
 
 // Does the row qualify, and its maximum M (from the fused kernel's slice
 // records: exact, the raw values being unpenalised).
-__device__ inline bool deep_eligible(const SampleArgs& A, int row, const cx_row_params& P,
-                                     double& M) {
+// (the conditions on the call and the row's parameters alone)
+__device__ inline bool deep_candidate(const SampleArgs& A, int row, const cx_row_params& P) {
   if (A.all_slow || A.out_probs) return false;
   if (!(P.temperature > 0.0) || P.typical_p < 1.0) return false;
   if (P.top_k > 0 && P.top_k < A.V) return false;
@@ -229,6 +229,11 @@ __device__ inline bool deep_eligible(const SampleArgs& A, int row, const cx_row_
   if (A.ldh > 0 && A.hist_len[row] > 0 &&
       (P.repetition_penalty != 1.0 || P.presence_penalty != 0.0 || P.frequency_penalty != 0.0))
     return false;
+  return true;
+}
+__device__ inline bool deep_eligible(const SampleArgs& A, int row, const cx_row_params& P,
+                                     double& M) {
+  if (!deep_candidate(A, row, P)) return false;
   double m = -__builtin_inf();
   for (int s = 0; s < A.nsplit; ++s) {
     const double v = A.stats[(size_t)row * A.nsplit + s].m;

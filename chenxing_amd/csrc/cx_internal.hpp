@@ -82,6 +82,8 @@ struct SampleArgs {
   int64_t ldo;
   int32_t slow_nbw;       // multi-pass kernel: full-row bitmap words (power of two)
   int32_t slow_off_hkey, slow_off_work, slow_off_tsum, slow_lds_bytes;
+  // slow_kernel takes only rows marked ROW_PENDING (after finish16_kernel)
+  int32_t pending_only;
 };
 
 // ---------------------------------------------------------------- verify

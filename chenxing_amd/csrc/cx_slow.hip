@@ -10,13 +10,17 @@
 //                     multi-pass path, as does any row the steps before
 //                     cannot decide; a pending top-p / min-p row without
 //                     top-k, typical-p or penalties first tries the
-//                     three-pass deep-nucleus path (cx_deep.hpp).  A
+//                     bucketed deep-nucleus path (cx_deep.hpp).  A
 //                     workgroup whose row is decided reads its status word
-//                     and exits.
+//                     and exits.  In a bf16 call it takes only the rows
+//                     finish16_kernel hands back.
+//   finish16_kernel   bf16 calls: the finisher and the refinement, then
+//                     deep-nucleus rows by counting values (cx_deep16.hpp)
 //   penalties_kernel  Sampler.apply_penalties, grid (rows, chunks of PEN_CHUNK)
 //   truncate_kernel   Sampler._truncate, one workgroup per row
 #include "cx_slow.hpp"
 #include "cx_deep.hpp"
+#include "cx_deep16.hpp"
 #include "cx_finish.hpp"
 #include "cx_timing.hpp"
 
@@ -59,7 +63,8 @@ __global__ __launch_bounds__(WG) void slow_kernel(SampleArgs A) {
   if (threadIdx.x == 0) {
     // a sliced row's status word is not written by the fused kernel
     const int st = A.row_status[row];
-    s_state = A.all_slow ? MULTIPASS
+    s_state = A.pending_only ? (st == ROW_PENDING ? MULTIPASS : DECIDED)
+              : A.all_slow ? MULTIPASS
               : (A.nsplit > 1 || st == ROW_FINISH) ? FINISH
               : st == ROW_PENDING ? MULTIPASS
               : st == ROW_REFINE ? REFINE : DECIDED;
@@ -79,6 +84,48 @@ __global__ __launch_bounds__(WG) void slow_kernel(SampleArgs A) {
   if (deep_row(A, row, dyn, red_d, red_i)) return;
   __syncthreads();
   slow_row(A, row, dyn, red_d, red_i);
+}
+
+// In place of slow_kernel's first part for a bf16 call: the region finisher
+// and the refinement as there, then, for a row still open, the counted
+// deep-nucleus path; a row none of them decides is marked ROW_PENDING for a
+// slow_kernel launch that takes only those.  (A kernel without the
+// multi-pass path: slow_kernel's register allocation stays as it is, and a
+// deep-nucleus row starts counting right after its finisher gives up.)
+// Grid 2B: workgroups are dispatched in order, so the first B take the rows
+// that may go deep (the long ones) and the last B the others, each exiting
+// at once on a row of the other kind.
+__global__ __launch_bounds__(WG) void finish16_kernel(SampleArgs A) {
+  extern __shared__ __align__(16) unsigned char dyn[];
+  __shared__ double red_d[2 * NWAVE + 4];
+  __shared__ int red_i[2 * NWAVE + 4];
+  __shared__ Deep16Shared sh;
+  __shared__ int s_state;
+  enum { DECIDED, OPEN, REFINE, FINISH };
+  const bool first = (int)blockIdx.x < A.B;
+  const int row = first ? (int)blockIdx.x : (int)blockIdx.x - A.B;
+  if (threadIdx.x == 0) {
+    // a sliced row's status word is not written by the fused kernel
+    const int st = A.row_status[row];
+    s_state = deep_candidate(A, row, A.prm[row]) != first ? DECIDED
+              : (A.nsplit > 1 || st == ROW_FINISH) ? FINISH
+              : st == ROW_PENDING ? OPEN
+              : st == ROW_REFINE ? REFINE : DECIDED;
+  }
+  __syncthreads();
+  int state = s_state;
+  if (state == DECIDED) return;
+  if (state == FINISH) {
+    const cx_row_params P = A.prm[row];
+    const int r = finish_row_fast<FIN_CAP>(A, row, P, dyn, red_d, red_i);
+    if (r == FIN_DONE) return;
+    state = r == FIN_REFINE ? REFINE : OPEN;
+    __syncthreads();
+  }
+  if (state == REFINE && refine_row(A, row, dyn, red_d, red_i)) return;
+  __syncthreads();
+  if (deep16_row(A, row, dyn, red_d, red_i, sh)) return;
+  if (threadIdx.x == 0) A.row_status[row] = ROW_PENDING;
 }
 
 __global__ __launch_bounds__(WG) void penalties_kernel(SampleArgs A) {
@@ -108,13 +155,23 @@ static int set_lds(K kernel, int bytes, int& attr) {
 }
 
 int launch_slow(const SampleArgs& A, hipStream_t s) {
-  static int attr = 0;
+  static int attr = 0, attr16 = 0;
   // the multi-pass layout, or a refined row's finisher region (which also
-  // holds the deep-nucleus path's tables)
+  // holds the deep-nucleus paths' tables and counters)
   static_assert(DEEP_LDS <= FIN_CAP * 32, "deep-nucleus LDS");
   const int bytes = max(A.slow_lds_bytes, FIN_CAP * 32);
   if (int e = set_lds(slow_kernel, bytes, attr)) return e;
-  timed_launch(CX_KERNEL_SAMPLE_SLOW, slow_kernel, dim3(A.B), dim3(WG), bytes, s, A);
+  SampleArgs A1 = A;
+  A1.pending_only = 0;
+  if (A.bf16 && !A.all_slow && !A.out_probs) {
+    // rows of a bf16 call may take the counted deep-nucleus path:
+    // finish16_kernel, then slow_kernel for the rows it hands back
+    if (int e = set_lds(finish16_kernel, FIN_CAP * 32, attr16)) return e;
+    timed_launch(CX_KERNEL_SAMPLE_SLOW, finish16_kernel, dim3(2 * A.B), dim3(WG), FIN_CAP * 32, s,
+                 A1);
+    A1.pending_only = 1;
+  }
+  timed_launch(CX_KERNEL_SAMPLE_SLOW, slow_kernel, dim3(A.B), dim3(WG), bytes, s, A1);
   return (int)hipGetLastError();
 }
 

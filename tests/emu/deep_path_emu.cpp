@@ -1,10 +1,10 @@
-// Runs the deep-nucleus row path (deep_row, cx_deep.hpp) on the host, one
-// workgroup at a time, with every buffer an exact-size heap allocation under
-// AddressSanitizer.  Each row's maximum goes into its slice record, as the
-// fused kernel leaves it.  Output per row: the sampled id, or -2 where the
-// path hands the row to the multi-pass path.
-// usage: deep_path_emu IN OUT (written and read by tests/test_emu_deep_path.py)
-#include "cx_deep.hpp"
+// Runs a deep-nucleus row path on the host (deep_row, cx_deep.hpp, or with
+// MODE 16 deep16_row, cx_deep16.hpp), one workgroup at a time, with every
+// buffer an exact-size heap allocation under AddressSanitizer.  Each row's
+// maximum goes into its slice record, as the fused kernel leaves it.  Output
+// per row: the sampled id, or -2 where the path hands the row back.
+// usage: deep_path_emu IN OUT [MODE] (written and read by tests/test_emu_deep_path.py)
+#include "cx_deep16.hpp"
 thread_local EmuDim threadIdx;
 EmuDim blockIdx;
 emu::Wave* emu::waves;
@@ -20,6 +20,8 @@ template <class T> static T* rd(FILE* f, size_t n) {
 int main(int argc, char** argv) {
   FILE* in = fopen(argv[1], "rb");
   FILE* out = fopen(argv[2], "wb");
+  const bool counted = argc > 3 && atoi(argv[3]) == 16;
+  const size_t lds = counted ? (size_t)FIN_CAP * 32 : (size_t)DEEP_LDS;
   int32_t ngroups;
   if (fread(&ngroups, 4, 1, in) != 1) return 2;
   for (int g = 0; g < ngroups; ++g) {
@@ -49,8 +51,8 @@ int main(int argc, char** argv) {
     A.nsplit = 1; A.stats = stats; A.bf16 = bf16; A.logV = log((double)V);
     A.vec_ok = ((uintptr_t)x % 16 == 0) && ((size_t)V * esz % 16 == 0);   // as the library sets it
     for (int row = 0; row < B; ++row) {
-      unsigned char* dyn = (unsigned char*)malloc(DEEP_LDS);
-      for (size_t i = 0; i < (size_t)DEEP_LDS; ++i) dyn[i] = (unsigned char)(i * 131 + 7);
+      unsigned char* dyn = (unsigned char*)malloc(lds);
+      for (size_t i = 0; i < lds; ++i) dyn[i] = (unsigned char)(i * 131 + 7);
       emu::Wave waves[16];
       emu::waves = waves;
       std::barrier<> bb(1024);
@@ -64,7 +66,9 @@ int main(int argc, char** argv) {
           threadIdx.x = t;
           __shared__ double red_d[2 * NWAVE + 4];
           __shared__ int red_i[2 * NWAVE + 4];
-          const bool r = deep_row(A, row, dyn, red_d, red_i);
+          __shared__ Deep16Shared sh;
+          const bool r = counted ? deep16_row(A, row, dyn, red_d, red_i, sh)
+                                 : deep_row(A, row, dyn, red_d, red_i);
           if (t == 0) decided = r ? 1 : 0;
           waves[t >> 6].bar.arrive_and_drop();
           bb.arrive_and_drop();

@@ -1,12 +1,13 @@
-"""The deep-nucleus row path (cx_deep.hpp ``deep_row``) compiled for the host
-and run under AddressSanitizer: one OS thread per work-item, a std::barrier
-per workgroup for __syncthreads, per-wave exchanges for ballots and
-shuffles (tests/emu/hip_emu.h).  Every LDS and global buffer is an
-exact-size heap allocation, so an out-of-bounds access fails the run.  On
-top-p / min-p rows with deep nuclei (fp32 rows of odd length, so most rows
-start unaligned, and bf16 rows full of ties) every row the path decides must
-sample the oracle's id; a row it hands back (-2) is allowed only where the
-test expects it (NaN).  CPU only."""
+"""The deep-nucleus row paths (cx_deep.hpp ``deep_row``, value buckets, and
+cx_deep16.hpp ``deep16_row``, counted bf16 values) compiled for the host and
+run under AddressSanitizer: one OS thread per work-item, a std::barrier per
+workgroup for __syncthreads, per-wave exchanges for ballots and shuffles
+(tests/emu/hip_emu.h).  Every LDS and global buffer is an exact-size heap
+allocation, so an out-of-bounds access fails the run.  On top-p / min-p rows
+with deep nuclei (fp32 rows of odd length, so most rows start unaligned, and
+bf16 rows full of ties) every row a path decides must sample the oracle's
+id; a row it hands back (-2) is allowed only where the test expects it.
+CPU only."""
 from __future__ import annotations
 
 import os
@@ -36,7 +37,7 @@ def _build(tmp: str) -> str:
     os.makedirs(os.path.join(tmp, "inc", "hip"))
     os.makedirs(src)
     shutil.copy(os.path.join(HERE, "emu", "hip_emu.h"), os.path.join(tmp, "inc", "hip", "hip_runtime.h"))
-    for f in ("cx_device.hpp", "cx_deep.hpp", "cx_internal.hpp"):
+    for f in ("cx_device.hpp", "cx_deep.hpp", "cx_deep16.hpp", "cx_internal.hpp"):
         text = open(os.path.join(CSRC, f)).read()
         text = re.sub(r"^#define CX_LDS __attribute__\(\(address_space\(3\)\)\)", "#define CX_LDS",
                       text, flags=re.M)
@@ -96,10 +97,7 @@ def _splits_a_tie(row: np.ndarray, prm: RowParams) -> bool:
     return int(np.sum(p[order[:cut]] == v)) < int(np.sum(p == v))
 
 
-def test_deep_path_emulated_on_deep_nucleus_rows():
-    groups = _groups()
-    kind, xb, prm, _, _ = groups[1]
-    assert any(_splits_a_tie(r, q) for r, q in zip(bf16_to_f32(xb), prm) if q.top_p < 1.0)
+def _run(groups, mode: int = 0):
     us = []
     with tempfile.TemporaryDirectory() as tmp:
         exe = _build(tmp)
@@ -113,9 +111,13 @@ def test_deep_path_emulated_on_deep_nucleus_rows():
                 f.write(struct.pack("iii", B, V, 1 if kind == "bf16" else 0))
                 for a in (x, pack_rows(prm), u.astype(np.float64)):
                     f.write(np.ascontiguousarray(a).tobytes())
-        r = subprocess.run([exe, fin, fout], capture_output=True, text=True, timeout=900)
+        r = subprocess.run([exe, fin, fout, str(mode)], capture_output=True, text=True, timeout=900)
         assert r.returncode == 0, r.stderr[-4000:]
         out = open(fout, "rb").read()
+    return _check(groups, us, out)
+
+
+def _check(groups, us, out) -> int:
     off = 0
     decided = 0
     for (kind, x, prm, back, _), u in zip(groups, us):
@@ -132,4 +134,31 @@ def test_deep_path_emulated_on_deep_nucleus_rows():
             assert res.status == R.STATUS_OK
             assert int(ids[b]) == res.token, (kind, b, int(ids[b]), res.token)
             decided += 1
-    assert decided == 19
+    return decided
+
+
+def test_deep_path_emulated_on_deep_nucleus_rows():
+    groups = _groups()
+    kind, xb, prm, _, _ = groups[1]
+    assert any(_splits_a_tie(r, q) for r, q in zip(bf16_to_f32(xb), prm) if q.top_p < 1.0)
+    assert _run(groups) == 19
+
+
+def test_counted_deep_path_emulated_on_bf16_rows():
+    """deep16_row: every bf16 row of the groups above decided by counting its
+    values (ties straddling the cut included), plus a row whose mask holds
+    more than 65535 ids (counted apart from the 16-bit counters), a row of
+    many signed zeros (one value), and a row with a value repeated 70000
+    times, whose counter would wrap: handed back."""
+    groups = [g for g in _groups() if g[0] == "bf16"]
+    rng = np.random.default_rng(11)
+    V = 100000
+    xb = f32_to_bf16_rne(rng.normal(0, 1.5, (3, V)).astype(np.float32))
+    xb[0, rng.choice(V, 70000, replace=False)] = 0xFF80          # -inf
+    xb[1, rng.choice(V, 3000, replace=False)] = 0x0000           # +0
+    xb[1, rng.choice(V, 3000, replace=False)] = 0x8000           # -0
+    xb[2, rng.choice(V, 70000, replace=False)] = f32_to_bf16_rne(np.float32([0.5]))[0]
+    prm = [RowParams(temperature=1.0, top_p=0.9), RowParams(temperature=2.0, top_p=0.7),
+           RowParams(temperature=1.0, top_p=0.9)]
+    groups.append(("bf16", xb, prm, {2}, None))
+    assert _run(groups, 16) == 11 + 2
