@@ -45,3 +45,36 @@ def test_deep_nucleus_rows(dtype, B, V):
     deep = int(np.sum((st & FLAG_DEEP) != 0))
     print(f"    {deep} of {B} rows by the deep-nucleus path", flush=True)
     assert deep >= (9 * B) // 10
+
+
+def test_counted_bf16_rows_and_hand_backs():
+    """bf16 rows through each branch of the counted deep-nucleus path
+    (cx_deep16.hpp): a value repeated 70000 times (its 16-bit counter wraps:
+    the row is handed back to the later paths), a mask of 100000 -inf ids
+    (counted apart), signed zeros (one value), a nucleus wider than the
+    copied window (a second pass over the row) and one through zero (the
+    three part tables), and min-p alone."""
+    rng = np.random.default_rng(77)
+    B, V = 8, 256000
+    x = rng.normal(0, 2.0, (B, V)).astype(np.float32)
+    for b in range(B):
+        x[b, rng.choice(V, 3, replace=False)] += np.float32(8.0)
+    xb = W.f32_to_bf16_rne(x)
+    xb[0, rng.choice(V, 70000, replace=False)] = W.f32_to_bf16_rne(np.float32([0.5]))[0]
+    xb[1, rng.choice(V, 100000, replace=False)] = 0xFF80
+    xb[2, :3000] = 0x0000
+    xb[2, 3000:6000] = 0x8000
+    prm = [RowParams(temperature=1.0, top_p=0.9), RowParams(temperature=1.0, top_p=0.9),
+           RowParams(temperature=2.0, top_p=0.8), RowParams(temperature=3.0, top_p=0.995),
+           RowParams(temperature=6.0, top_p=0.999), RowParams(temperature=1.0, top_p=1.0, min_p=0.01),
+           RowParams(temperature=0.7, top_p=0.95, min_p=0.001), RowParams(temperature=1.2, top_p=0.6)]
+    w = W.SampleWorkload("counted_bf16", xb, "bf16", prm, np.zeros((B, 0), np.int32),
+                         np.zeros(B, np.int32), rng.random(B))
+    print("[gpu] counted bf16 rows B=8 V=256000", flush=True)
+    ids, st, _ = sample_host(w.logits, w.params, None, None, w.u, bf16=True)
+    print("    status flags per row:", [hex(int(v) & 0xF00) for v in st], flush=True)
+    pairs = oracle_rows_parallel(w, ties=("stable", "numpy"))
+    t = compare_rows(ids, st, None, [p[0] for p in pairs], "counted_bf16[B=8]",
+                     ref_rows=[p[1] for p in pairs])
+    assert not t.mismatches, t.mismatches[:5]
+    assert t.draws == B and t.boundary == 0
