@@ -580,13 +580,14 @@ __device__ inline bool deep_row_impl(const SampleArgs& A, int row, const cx_row_
   return true;
 }
 
-// The exact normaliser sum over the row of exp((x - M) / T), in fp64 with
-// the table-driven exp, for a row without a penalty window: the passes'
-// stream (loads three steps ahead) instead of one load round trip per eight
+// The exact normaliser sum over the row's ids [lo, hi) (lo a multiple of
+// 16384; the whole row by default) of exp((x - M) / T), in fp64 with the
+// table-driven exp, for a row without a penalty window: the passes' stream
+// (loads three steps ahead) instead of one load round trip per eight
 // elements.  The same value on every thread.
 template <bool VEC>
 __device__ inline double deep_exact_sum_impl(const SampleArgs& A, int row, double M, double invT,
-                                             double* red_d) {
+                                             double* red_d, int lo, int hi) {
   __shared__ double etab[64];
   load_exp64_tab(etab);
   DeepRow R;
@@ -598,22 +599,23 @@ __device__ inline double deep_exact_sum_impl(const SampleArgs& A, int row, doubl
   R.rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(R.p), (short)0,
                                            (R.V * (R.bf16 ? 2 : 4) + 15) & ~15, 0x00020000);
   const int t = threadIdx.x;
+  hi = min(hi, R.V);
   double s = 0.0;
-  deep_stream<VEC>(R, 0, R.step, t, (R.V + R.step - 1) / R.step,
+  deep_stream<VEC>(R, lo, R.step, t, (hi - lo + R.step - 1) / R.step,
                    [&](int k, const uint32_t (&wd)[DW]) {
-    const int e0 = k * R.step + R.nv * t;
+    const int e0 = lo + k * R.step + R.nv * t;
 #pragma unroll
     for (int j = 0; j < DNV; ++j) {
-      if (j >= R.nv || e0 + j >= R.V) break;
+      if (j >= R.nv || e0 + j >= hi) break;
       s += exp64_neg(((double)deep_val(R, wd, j) - M) * invT, etab);
     }
   });
   return block_sum(s, red_d);
 }
 __device__ inline double deep_exact_sum(const SampleArgs& A, int row, double M, double invT,
-                                        double* red_d) {
-  return A.vec_ok ? deep_exact_sum_impl<true>(A, row, M, invT, red_d)
-                  : deep_exact_sum_impl<false>(A, row, M, invT, red_d);
+                                        double* red_d, int lo = 0, int hi = INT_MAX) {
+  return A.vec_ok ? deep_exact_sum_impl<true>(A, row, M, invT, red_d, lo, hi)
+                  : deep_exact_sum_impl<false>(A, row, M, invT, red_d, lo, hi);
 }
 
 // Samples the row and returns true, or returns false with nothing written

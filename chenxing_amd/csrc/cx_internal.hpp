@@ -44,7 +44,8 @@ struct SplitStats {       // one per (row, slice), 64 bytes
   uint32_t tau;           // region threshold key; <= 1 means the region is the whole slice
   int32_t ncand;          // region entries written to the workspace
   int32_t flags;
-  int32_t pad1[3];
+  int32_t pad1;
+  double xshare;          // slow_kernel: this part's share of the row's exact normaliser
 };
 static_assert(sizeof(SplitStats) == 64, "SplitStats layout");
 
@@ -66,7 +67,7 @@ struct SampleArgs {
   int32_t* out_id;
   int32_t* row_status;
   float* out_probs;
-  int32_t* counters;      // [B], zero between calls (unused by the kernels)
+  int32_t* counters;      // [B] sliced rows: exact-normaliser shares summed (zeroed by the fused kernel)
   SplitStats* stats;      // [B * nsplit]
   Cand* cands;            // [B * nsplit * CAPS]
   int32_t nsplit, split_len;
@@ -84,6 +85,9 @@ struct SampleArgs {
   int32_t slow_off_hkey, slow_off_work, slow_off_tsum, slow_lds_bytes;
   // slow_kernel takes only rows marked ROW_PENDING (after finish16_kernel)
   int32_t pending_only;
+  // slow_kernel's grid is B * nsplit: the workgroups of a sliced top-p row
+  // each sum a share of its exact normaliser, the last to finish takes the row
+  int32_t par_exact;
 };
 
 // ---------------------------------------------------------------- verify

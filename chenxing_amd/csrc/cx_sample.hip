@@ -987,6 +987,9 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   const int ch0 = __builtin_amdgcn_readfirstlane(wave_id());
   typename E::V q[U], qn[U];
   load_chunk<BF16>(rs, ch0, q);
+  // slow_kernel's count of a sliced row's exact-normaliser shares starts at
+  // zero (the workspace may hold a previous call's records of another layout)
+  if (!single && split == 0 && t == 0) A.counters[row] = 0;
 
   // the row's parameters live in LDS after the first barrier (P), not in
   // registers across the stream; P0 serves the prologue

@@ -81,28 +81,30 @@ __device__ __forceinline__ double value_at(const SlowRow& R, int i) {
   return penalise_at(R, i, raw_at(R, i));
 }
 
-// sum over the row of exp((x - M) / T), x the penalised fp64 values (the
-// reference's normaliser, sampler.py:119-123), in fp64, with the
-// table-driven exp (within 1 ulp; every argument is <= 0).  Every thread
-// keeps EXN independent loads in flight per step; the result is the same on
-// every thread.
-__device__ inline double exact_norm(const SlowRow& R, double M, double invT, double* red_d) {
+// sum over the row's ids [lo, hi) (the whole row by default) of
+// exp((x - M) / T), x the penalised fp64 values (the reference's normaliser,
+// sampler.py:119-123), in fp64, with the table-driven exp (within 1 ulp;
+// every argument is <= 0).  Every thread keeps EXN independent loads in
+// flight per step; the result is the same on every thread.
+__device__ inline double exact_norm(const SlowRow& R, double M, double invT, double* red_d,
+                                   int lo = 0, int hi = INT_MAX) {
   constexpr int EXN = 8;
   __shared__ double etab[64];
   load_exp64_tab(etab);
   const int t = threadIdx.x;
+  hi = min(hi, R.V);
   double s = 0.0;
-  for (int base = 0; base < R.V; base += EXN * WG) {
+  for (int base = lo; base < hi; base += EXN * WG) {
     double x[EXN];
 #pragma unroll
     for (int j = 0; j < EXN; ++j) {
       const int i = base + j * WG + t;
-      x[j] = i < R.V ? raw_at(R, i) : 0.0;
+      x[j] = i < hi ? raw_at(R, i) : 0.0;
     }
 #pragma unroll
     for (int j = 0; j < EXN; ++j) {
       const int i = base + j * WG + t;
-      if (i < R.V) s += exp64_neg((penalise_at(R, i, x[j]) - M) * invT, etab);
+      if (i < hi) s += exp64_neg((penalise_at(R, i, x[j]) - M) * invT, etab);
     }
   }
   return block_sum(s, red_d);
