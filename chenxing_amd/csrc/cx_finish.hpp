@@ -75,6 +75,20 @@ __device__ inline uint64_t kth_candidate_key(const SampleArgs& A, int row, uint6
 // buckets' weights are summed as fixed-point integers with LDS atomics
 // (exact, so independent of the order of the additions), scanned, and only
 // the bucket that holds the cut is gathered, sorted by one wave and scanned.
+// A slot, counted from *counter, for each lane of the wave with p set, in
+// lane order: one LDS atomic per wave instead of one per element.  Every
+// lane of the wave calls it.
+__device__ __forceinline__ int wave_append_slot(bool p, int* counter) {
+  const uint64_t b = ballot(p);
+  int base = 0;
+  if (b) {
+    const int first = __builtin_ctzll(b);
+    if (lane_id() == first) base = atomicAdd(counter, __popcll(b));
+    base = __shfl(base, first);
+  }
+  return base + lanes_below(b);
+}
+
 constexpr int NBK = WG;            // buckets: one per thread in the scan
 constexpr int GBK = 64;            // a gathered bucket: one entry per lane
 constexpr double FX_MASS = 1152921504606846976.0;   // 2^60: masses sum to <= ~1
@@ -146,11 +160,12 @@ __device__ inline void prefix_cut(int E, const int32_t* sidx, BucketOf bucket_of
   }
   if (t == bc) red_u[2 * NWAVE + 1] = base;          // the weight before the cut bucket
   // gather the cut bucket
-  for (int j = t; j < E; j += WG)
-    if (elig(j) && bucket_of(j) == bc) {
-      const int q = atomicAdd(&pc_n, 1);
-      if (q < GBK) { gk[q] = key_of(j); gi[q] = sidx[j]; ga[q] = j; }
-    }
+  for (int j0 = 0; j0 < E; j0 += WG) {
+    const int j = j0 + t;
+    const bool p = j < E && elig(j) && bucket_of(j) == bc;
+    const int q = wave_append_slot(p, &pc_n);
+    if (p && q < GBK) { gk[q] = key_of(j); gi[q] = sidx[j]; ga[q] = j; }
+  }
   __syncthreads();
   const int n = pc_n;
   if (n > GBK) {
@@ -386,13 +401,26 @@ __device__ inline int finish_row_fast(const SampleArgs& A, int row, const cx_row
   }
   __syncthreads();
   const int ncand = f_off[nsp];
-  for (int g = t; g < ncand; g += WG) {
-    int s = 0;
-    while (g >= f_off[s + 1]) ++s;
-    const Cand c = A.cands[((size_t)row * nsp + s) * CAPS + (g - f_off[s])];
-    if (c.key >= thr64) {
-      const int pos = atomicAdd(&f_n, 1);
-      if (pos < CAP) { skey[pos] = c.key; sidx[pos] = c.idx; saux[pos] = 0; }
+  // R candidates per thread per round, their loads issued together (uniform
+  // trips: whole waves append)
+  for (int g0 = 0; g0 < ncand; g0 += R * WG) {
+    Cand c[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int g = g0 + r * WG + t;
+      c[r].key = 0ull;
+      c[r].idx = 0;
+      if (g < ncand) {
+        int s = 0;
+        while (g >= f_off[s + 1]) ++s;
+        c[r] = A.cands[((size_t)row * nsp + s) * CAPS + (g - f_off[s])];
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const bool p = g0 + r * WG + t < ncand && c[r].key >= thr64;
+      const int pos = wave_append_slot(p, &f_n);
+      if (p && pos < CAP) { skey[pos] = c[r].key; sidx[pos] = c[r].idx; saux[pos] = 0; }
     }
   }
   __syncthreads();
@@ -409,12 +437,15 @@ __device__ inline int finish_row_fast(const SampleArgs& A, int row, const cx_row
     for (int s = 0; s < nsp; ++s) {
       const Cand* cs = A.cands + ((size_t)row * nsp + s) * CAPS;
       const int n = st[s].ncand;
-      for (int e = t; e < n; e += WG) {
-        Cand c = cs[e];
-        if (c.key >= thr2) {
-          int pos = atomicAdd(&f_n, 1);
-          if (pos < CAP) { skey[pos] = c.key; sidx[pos] = c.idx; saux[pos] = 0; }
-        }
+      for (int e0 = 0; e0 < n; e0 += WG) {
+        const int e = e0 + t;
+        Cand c;
+        c.key = 0ull;
+        c.idx = 0;
+        if (e < n) c = cs[e];
+        const bool p = e < n && c.key >= thr2;
+        const int pos = wave_append_slot(p, &f_n);
+        if (p && pos < CAP) { skey[pos] = c.key; sidx[pos] = c.idx; saux[pos] = 0; }
       }
     }
     __syncthreads();
