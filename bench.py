@@ -56,6 +56,20 @@ def _say(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
+def copy_probe(dev) -> None:
+    """Five 512 MiB device-to-device copies (torch copy_): a kernel whose HBM
+    traffic is known exactly, to scale FETCH_SIZE / WRITE_SIZE counters."""
+    import torch
+    _say("[bench] copy probe: 5 x 512 MiB device copy")
+    src = torch.ones(128 << 20, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    torch.cuda.empty_cache()
+
+
 # Inputs are rotated over enough copies to exceed twice MI355X's 256 MB
 # Infinity Cache, so a timed step reads its logits from HBM, not from the
 # cache the previous step filled.
@@ -305,6 +319,8 @@ def main() -> int:
         _lib.load()
         _say(f"[bench] {args.only}")
         entry = time_other(args.only, torch.device("cuda:0"), args.steps, args.warmup)
+        if args.copy_probe:
+            copy_probe(torch.device("cuda:0"))
         print(json.dumps({"workload": args.only, "steps": args.steps, **entry}), flush=True)
         return 0
     _say("[bench] generating full_penalty workload")
@@ -361,14 +377,7 @@ def main() -> int:
                                      max(5, args.warmup // 5))
 
     if args.copy_probe:
-        _say("[bench] copy probe: 5 x 512 MiB device copy")
-        src = torch.ones(128 << 20, dtype=torch.float32, device=dev)
-        dst = torch.empty_like(src)
-        for _ in range(5):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
-        torch.cuda.empty_cache()
+        copy_probe(dev)
 
     out = {
         "metric": METRIC,

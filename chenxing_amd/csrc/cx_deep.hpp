@@ -590,8 +590,11 @@ __device__ inline double deep_exact_sum_impl(const SampleArgs& A, int row, doubl
                                              double* red_d, int lo, int hi) {
   __shared__ double etab[64];
   load_exp64_tab(etab);
+  // the row as far as hi: the loads the stream issues past hi return zeros
+  // and read nothing (not the next share's logits)
+  hi = min(hi, A.V);
   DeepRow R;
-  R.V = A.V;
+  R.V = hi;
   R.bf16 = A.bf16 != 0;
   R.nv = R.bf16 ? 16 : 8;
   R.step = R.nv * WG;
@@ -599,7 +602,6 @@ __device__ inline double deep_exact_sum_impl(const SampleArgs& A, int row, doubl
   R.rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(R.p), (short)0,
                                            (R.V * (R.bf16 ? 2 : 4) + 15) & ~15, 0x00020000);
   const int t = threadIdx.x;
-  hi = min(hi, R.V);
   double s = 0.0;
   deep_stream<VEC>(R, lo, R.step, t, (hi - lo + R.step - 1) / R.step,
                    [&](int k, const uint32_t (&wd)[DW]) {
