@@ -67,7 +67,12 @@ struct SampleArgs {
   int32_t* out_id;
   int32_t* row_status;
   float* out_probs;
-  int32_t* counters;      // [B] sliced rows: exact-normaliser shares summed (zeroed by the fused kernel)
+  // [B + 1], each written by the fused kernel before the later kernels read
+  // it: [row] of a sliced row, its exact-normaliser shares summed (zeroed);
+  // [row] of a single-slice row, its hand-off mark (ROW_FINISH, ROW_REFINE,
+  // ROW_PENDING, or 0 if decided), which, unlike row_status, the finishing
+  // kernels leave as it is; [B], finish16_kernel's work-item counter (zeroed)
+  int32_t* counters;
   SplitStats* stats;      // [B * nsplit]
   Cand* cands;            // [B * nsplit * CAPS]
   int32_t nsplit, split_len;
@@ -202,7 +207,7 @@ inline VerifyWorkspace verify_workspace_layout(int B, int gamma, int V) {
 inline SampleWorkspace sample_workspace_layout(int B, int ns) {
   SampleWorkspace w;
   w.off_counters = 0;
-  w.off_stats = align_up((size_t)B * 4, 256);
+  w.off_stats = align_up((size_t)(B + 1) * 4, 256);
   w.off_cands = align_up(w.off_stats + (size_t)B * ns * sizeof(SplitStats), 256);
   w.total = align_up(w.off_cands + (size_t)B * ns * CAPS * sizeof(Cand), 256);
   return w;

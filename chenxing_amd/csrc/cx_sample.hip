@@ -988,8 +988,11 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   typename E::V q[U], qn[U];
   load_chunk<BF16>(rs, ch0, q);
   // slow_kernel's count of a sliced row's exact-normaliser shares starts at
-  // zero (the workspace may hold a previous call's records of another layout)
-  if (!single && split == 0 && t == 0) A.counters[row] = 0;
+  // zero (the workspace may hold a previous call's records of another
+  // layout), as do a single-slice row's hand-off mark and finish16_kernel's
+  // work-item counter
+  if (split == 0 && t == 0) A.counters[row] = 0;
+  if (blockIdx.x == 0 && t == 0) A.counters[A.B] = 0;
 
   // the row's parameters live in LDS after the first barrier (P), not in
   // registers across the stream; P0 serves the prologue
@@ -1266,8 +1269,10 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
       }
     }
     if (lane_id() == 0) {
+      const int mark = dr == LEAN_DONE ? 0 : (dr == LEAN_NEAR ? ROW_REFINE : ROW_PENDING);
       A.out_id[row] = dr == LEAN_DONE ? tok : -1;
-      A.row_status[row] = dr == LEAN_DONE ? CX_ROW_OK : (dr == LEAN_NEAR ? ROW_REFINE : ROW_PENDING);
+      A.row_status[row] = mark ? mark : CX_ROW_OK;
+      A.counters[row] = mark;
     }
     return;
   }
@@ -1350,7 +1355,10 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   // per-workgroup cache writebacks, and the finisher's registers stay out of
   // this kernel.  Sliced rows are always finished there; a single-slice row
   // is marked.
-  if (single && t == 0) A.row_status[row] = ROW_FINISH;
+  if (single && t == 0) {
+    A.row_status[row] = ROW_FINISH;
+    A.counters[row] = ROW_FINISH;
+  }
 }
 
 template __global__ void sample_kernel<false>(SampleArgs);

@@ -15,7 +15,8 @@
 //                     and exits.  In a bf16 call it takes only the rows
 //                     finish16_kernel hands back.
 //   finish16_kernel   bf16 calls: the finisher and the refinement, then
-//                     deep-nucleus rows by counting values (cx_deep16.hpp)
+//                     deep-nucleus rows by counting values (cx_deep16.hpp);
+//                     each workgroup takes its row from a counter
 //   penalties_kernel  Sampler.apply_penalties, grid (rows, chunks of PEN_CHUNK)
 //   truncate_kernel   Sampler._truncate, one workgroup per row
 #include "cx_slow.hpp"
@@ -143,35 +144,80 @@ __global__ __launch_bounds__(WG) void slow_kernel(SampleArgs A) {
   slow_row(A, row, dyn, red_d, red_i);
 }
 
+// finish16_kernel's work items: 0 for a row with nothing left to do, 1 for
+// a row that may go deep (the long ones), 2 for another row with work.  From
+// the fused kernel's hand-off marks, which nothing changes during the kernel
+// (a sliced row's are all finished).  A pending row that cannot go deep is
+// left to slow_kernel as it is.
+__device__ inline int f16_class(const SampleArgs& A, int row) {
+  const int mark = A.nsplit > 1 ? ROW_FINISH : A.counters[row];
+  const bool deep = deep_candidate(A, row, A.prm[row]);
+  if (mark == ROW_FINISH || mark == ROW_REFINE) return deep ? 1 : 2;
+  return mark == ROW_PENDING && deep ? 1 : 0;
+}
+
+// The row of item idx of finish16_kernel's list: the class-1 rows in row
+// order, then the class-2 rows (nd of class 1).  Every thread gets it.
+// cnt: NWAVE ints; out: one int.
+__device__ inline int f16_item_row(const SampleArgs& A, int idx, int nd, int* cnt, int* out) {
+  const int want = idx < nd ? 1 : 2;
+  const int target = idx < nd ? idx : idx - nd;
+  const int t = threadIdx.x, w = wave_id();
+  int base = 0;                                   // items of that class in earlier chunks
+  if (t == 0) *out = -1;                          // (ordered by the loop's first barrier)
+  for (int c = 0; c < A.B && base <= target; c += WG) {
+    const bool is = c + t < A.B && f16_class(A, c + t) == want;
+    const uint64_t b = ballot(is);
+    if (lane_id() == 0) cnt[w] = __popcll(b);
+    __syncthreads();
+    int below = base, tot = 0;
+    for (int j = 0; j < NWAVE; ++j) {
+      const int n = cnt[j];
+      below += j < w ? n : 0;
+      tot += n;
+    }
+    if (is && below + lanes_below(b) == target) *out = c + t;
+    base += tot;
+    __syncthreads();
+  }
+  return *out;
+}
+
 // In place of slow_kernel's first part for a bf16 call: the region finisher
 // and the refinement as there, then, for a row still open, the counted
 // deep-nucleus path; a row none of them decides is marked ROW_PENDING for a
 // slow_kernel launch that takes only those.  (A kernel without the
 // multi-pass path: slow_kernel's register allocation stays as it is, and a
 // deep-nucleus row starts counting right after its finisher gives up.)
-// Grid 2B: workgroups are dispatched in order, so the first B take the rows
-// that may go deep (the long ones) and the last B the others, each exiting
-// at once on a row of the other kind.
+// Grid B: each workgroup takes the next work item from a counter, in the
+// order the workgroups start, so the rows that may go deep (the long ones)
+// start together on the first workgroups, the others follow on the CUs as
+// they free up, and the workgroups left without an item exit last.  (With
+// one workgroup per row and kind, blockIdx order, some deep rows started
+// 40 us late, behind workgroups that only read a status word and exit.)
 __global__ __launch_bounds__(WG) void finish16_kernel(SampleArgs A) {
   extern __shared__ __align__(16) unsigned char dyn[];
   __shared__ double red_d[2 * NWAVE + 4];
   __shared__ int red_i[2 * NWAVE + 4];
   __shared__ Deep16Shared sh;
-  __shared__ int s_state;
-  enum { DECIDED, OPEN, REFINE, FINISH };
-  const bool first = (int)blockIdx.x < A.B;
-  const int row = first ? (int)blockIdx.x : (int)blockIdx.x - A.B;
-  if (threadIdx.x == 0) {
-    // a sliced row's status word is not written by the fused kernel
-    const int st = A.row_status[row];
-    s_state = deep_candidate(A, row, A.prm[row]) != first ? DECIDED
-              : (A.nsplit > 1 || st == ROW_FINISH) ? FINISH
-              : st == ROW_PENDING ? OPEN
-              : st == ROW_REFINE ? REFINE : DECIDED;
+  __shared__ int s_item[2];
+  enum { OPEN, REFINE, FINISH };
+  const int t = threadIdx.x;
+  if (t == 0) s_item[0] = atomicAdd(A.counters + A.B, 1);
+  int nd = 0, nw = 0;
+  for (int c = 0; c < A.B; c += WG) {
+    const int cls = c + t < A.B ? f16_class(A, c + t) : 0;
+    nd += cls == 1;
+    nw += cls != 0;
   }
-  __syncthreads();
-  int state = s_state;
-  if (state == DECIDED) return;
+  nd = block_sum(nd, red_i);                      // (its barriers also publish s_item[0])
+  nw = block_sum(nw, red_i);
+  const int idx = s_item[0];
+  if (idx >= nw) return;
+  const int row = f16_item_row(A, idx, nd, red_i, s_item + 1);
+  if (row < 0) return;                            // (every workgroup's list is the same)
+  const int mark = A.nsplit > 1 ? ROW_FINISH : A.counters[row];
+  int state = mark == ROW_FINISH ? FINISH : mark == ROW_REFINE ? REFINE : OPEN;
   if (state == FINISH) {
     const cx_row_params P = A.prm[row];
     const int r = finish_row_fast<FIN_CAP>(A, row, P, dyn, red_d, red_i);
@@ -182,7 +228,7 @@ __global__ __launch_bounds__(WG) void finish16_kernel(SampleArgs A) {
   if (state == REFINE && refine_row(A, row, dyn, red_d, red_i)) return;
   __syncthreads();
   if (deep16_row(A, row, dyn, red_d, red_i, sh)) return;
-  if (threadIdx.x == 0) A.row_status[row] = ROW_PENDING;
+  if (t == 0) A.row_status[row] = ROW_PENDING;
 }
 
 __global__ __launch_bounds__(WG) void penalties_kernel(SampleArgs A) {
@@ -225,7 +271,7 @@ int launch_slow(const SampleArgs& A, hipStream_t s) {
     // rows of a bf16 call may take the counted deep-nucleus path:
     // finish16_kernel, then slow_kernel for the rows it hands back
     if (int e = set_lds(finish16_kernel, FIN_CAP * 32, attr16)) return e;
-    timed_launch(CX_KERNEL_SAMPLE_SLOW, finish16_kernel, dim3(2 * A.B), dim3(WG), FIN_CAP * 32, s,
+    timed_launch(CX_KERNEL_SAMPLE_SLOW, finish16_kernel, dim3(A.B), dim3(WG), FIN_CAP * 32, s,
                  A1);
     A1.pending_only = 1;
   } else if (A.nsplit > 1 && !A.all_slow) {
