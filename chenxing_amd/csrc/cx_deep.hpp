@@ -602,17 +602,29 @@ __device__ inline double deep_exact_sum_impl(const SampleArgs& A, int row, doubl
   R.rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(R.p), (short)0,
                                            (R.V * (R.bf16 ? 2 : 4) + 15) & ~15, 0x00020000);
   const int t = threadIdx.x;
-  double s = 0.0;
+  // per step, the fetch's values as straight-line code (a loop bounded by
+  // R.nv, with a break at hi, ran its exps one after another): four
+  // accumulators, element j into j % 4, values at or past hi selected away
+  double s[4] = {0.0, 0.0, 0.0, 0.0};
   deep_stream<VEC>(R, lo, R.step, t, (hi - lo + R.step - 1) / R.step,
                    [&](int k, const uint32_t (&wd)[DW]) {
     const int e0 = lo + k * R.step + R.nv * t;
+    if (R.bf16) {
 #pragma unroll
-    for (int j = 0; j < DNV; ++j) {
-      if (j >= R.nv || e0 + j >= hi) break;
-      s += exp64_neg(((double)deep_val(R, wd, j) - M) * invT, etab);
+      for (int j = 0; j < 16; ++j) {
+        const float x = __uint_as_float((j & 1) ? (wd[j >> 1] & 0xFFFF0000u) : (wd[j >> 1] << 16));
+        const double e = exp64_neg(((double)x - M) * invT, etab);
+        s[j & 3] += e0 + j < hi ? e : 0.0;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const double e = exp64_neg(((double)__uint_as_float(wd[j]) - M) * invT, etab);
+        s[j & 3] += e0 + j < hi ? e : 0.0;
+      }
     }
   });
-  return block_sum(s, red_d);
+  return block_sum((s[0] + s[1]) + (s[2] + s[3]), red_d);
 }
 __device__ inline double deep_exact_sum(const SampleArgs& A, int row, double M, double invT,
                                         double* red_d, int lo = 0, int hi = INT_MAX) {

@@ -32,6 +32,7 @@
 #include "cx_sampler.h"
 #include "cx_internal.hpp"
 #include "cx_finish.hpp"
+#include "cx_deep.hpp"
 #include "cx_timing.hpp"
 
 namespace cx {
@@ -1272,7 +1273,7 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
       const int mark = dr == LEAN_DONE ? 0 : (dr == LEAN_NEAR ? ROW_REFINE : ROW_PENDING);
       A.out_id[row] = dr == LEAN_DONE ? tok : -1;
       A.row_status[row] = mark ? mark : CX_ROW_OK;
-      A.counters[row] = mark;
+      A.counters[row] = mark | (mark && deep_candidate(A, row, P) ? MARK_DEEP : 0);
     }
     return;
   }
@@ -1357,7 +1358,7 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   // is marked.
   if (single && t == 0) {
     A.row_status[row] = ROW_FINISH;
-    A.counters[row] = ROW_FINISH;
+    A.counters[row] = ROW_FINISH | (deep_candidate(A, row, P) ? MARK_DEEP : 0);
   }
 }
 

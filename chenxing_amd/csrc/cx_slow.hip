@@ -146,12 +146,15 @@ __global__ __launch_bounds__(WG) void slow_kernel(SampleArgs A) {
 
 // finish16_kernel's work items: 0 for a row with nothing left to do, 1 for
 // a row that may go deep (the long ones), 2 for another row with work.  From
-// the fused kernel's hand-off marks, which nothing changes during the kernel
-// (a sliced row's are all finished).  A pending row that cannot go deep is
-// left to slow_kernel as it is.
+// the fused kernel's hand-off marks (one load), which nothing changes during
+// the kernel; a sliced row's are all finished, the deep test from its
+// parameters.  A pending row that cannot go deep is left to slow_kernel as
+// it is.
 __device__ inline int f16_class(const SampleArgs& A, int row) {
-  const int mark = A.nsplit > 1 ? ROW_FINISH : A.counters[row];
-  const bool deep = deep_candidate(A, row, A.prm[row]);
+  const int m = A.nsplit > 1 ? (ROW_FINISH | (deep_candidate(A, row, A.prm[row]) ? MARK_DEEP : 0))
+                             : A.counters[row];
+  const int mark = m & ~MARK_DEEP;
+  const bool deep = (m & MARK_DEEP) != 0;
   if (mark == ROW_FINISH || mark == ROW_REFINE) return deep ? 1 : 2;
   return mark == ROW_PENDING && deep ? 1 : 0;
 }
@@ -216,7 +219,7 @@ __global__ __launch_bounds__(WG) void finish16_kernel(SampleArgs A) {
   if (idx >= nw) return;
   const int row = f16_item_row(A, idx, nd, red_i, s_item + 1);
   if (row < 0) return;                            // (every workgroup's list is the same)
-  const int mark = A.nsplit > 1 ? ROW_FINISH : A.counters[row];
+  const int mark = A.nsplit > 1 ? ROW_FINISH : A.counters[row] & ~MARK_DEEP;
   int state = mark == ROW_FINISH ? FINISH : mark == ROW_REFINE ? REFINE : OPEN;
   if (state == FINISH) {
     const cx_row_params P = A.prm[row];
