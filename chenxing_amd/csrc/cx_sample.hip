@@ -1064,8 +1064,14 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   __syncthreads();
   const int nd = pen_on ? s_nd : 0;
   CX_LDS int* const gctr = to_lds(&s_gctr);
+  // A single-slice bf16 row that may take the counted deep-nucleus path
+  // (finish16_kernel counts its values from its maximum on, and decides it
+  // exactly or hands it to the exact path) needs only its maximum here: the
+  // greedy stream, with no region.  (Its region would be a candidate list
+  // its nucleus usually outgrows.)
+  const bool count_row = BF16 && single && !greedy && !A.out_probs && deep_candidate(A, row, P);
   // ---------------------------------------------------------------- greedy
-  if (greedy) {
+  if (greedy || count_row) {
     GreedyState gs{-__builtin_inff(), INT_MAX, INT_MAX};
     stream_greedy<BF16>(rowp, rs, q, qn, nv, lo, hi, s0, pen_on, X, to_lds(&s_chunk), gs);
     double bv = gs.bi == INT_MAX ? -__builtin_inf() : (double)gs.bv;
@@ -1086,7 +1092,15 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
     }
     block_argmax(bv, bi, red_d, red_i);
     ni = block_min(ni, red_i, INT_MAX);
-    if (single) {
+    if (count_row) {
+      if (t == 0) {
+        my->m = bv; my->s = 0; my->tol = 0; my->best_v = bv; my->best_i = bi; my->nan_i = ni;
+        my->tau = 1u; my->ncand = 0; my->flags = 0;
+        A.out_id[row] = -1;
+        A.row_status[row] = ROW_PENDING;
+        A.counters[row] = ROW_PENDING | MARK_DEEP;
+      }
+    } else if (single) {
       const int tok = ni != INT_MAX ? ni : (bi == INT_MAX ? 0 : bi);
       write_row_result(A, row, CX_ROW_GREEDY, tok);
       write_one_hot(A, row, tok);
