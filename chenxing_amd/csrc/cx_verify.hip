@@ -555,6 +555,22 @@ __global__ __launch_bounds__(WG) void verify_norm(VerifyArgs A) {
 }
 
 // ------------------------------------------------------------ 4. draw
+// Partials s0, s0 + 64, s0 + 128, s0 + 192 of a sequence (indices past ns
+// read the last one, unused), loaded together.
+__device__ __forceinline__ void load_parts(const NormPart* np, int ns, int s0, double (&se)[4],
+                                           double (&sf)[4], double (&dp)[4], double (&fp)[4],
+                                           int (&na)[4]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const NormPart& P = np[min(s0 + 64 * j, ns - 1)];
+    se[j] = P.se;
+    sf[j] = P.sf;
+    dp[j] = P.dp;
+    fp[j] = P.fp;
+    na[j] = P.namb;
+  }
+}
+
 // numpy's choice(V, p=r/R) with r = max(p - q, 0) (speculative.py:161-166).
 // With e, f the exp terms of the rejected row pair, St, Sq their exact sums
 // and lam = St / Sq, r = St^-1 w with w = max(e - lam f, 0): the draw runs on
@@ -572,15 +588,20 @@ __global__ __launch_bounds__(WG) void verify_draw(VerifyArgs A) {
   const int t = threadIdx.x;
   const float T = A.temperature[b];
   const SeqState q = A.seq[b];
-  load_exp64_tab(tab);                                // in flight with the state
+  const int ns = A.nsub;                              // <= 2 * WG
+  const NormPart* np = A.npart + (size_t)b * ns;
+  // wave 0's first four partials per lane, in flight with the state and the
+  // table (the workspace holds them whether or not the row draws)
+  double pse[4], psf[4], pdp[4], pfp[4];
+  int pna[4];
+  if (wave_id() == 0) load_parts(np, ns, lane_id(), pse, psf, pdp, pfp, pna);
+  load_exp64_tab(tab);
   if (T == 0.0f || q.rej1 == 0) return;
   const int r = q.rej1 - 1;
   const int g = A.gamma;
-  const int ns = A.nsub;                              // <= 2 * WG
   const float* tr = trow(A, b, r);
   const float* dr = drow(A, b, r);
   const double u = A.u[(size_t)b * (g + 1) + r + 1];
-  const NormPart* np = A.npart + (size_t)b * ns;
   ResidCtx C;
   C.invT = 1.0 / (double)T;
   C.zmt = q.Mt / T;
@@ -594,16 +615,23 @@ __global__ __launch_bounds__(WG) void verify_draw(VerifyArgs A) {
   // leave the row to the block-wide exact redo below.
   if (wave_id() == 0) {
     const int l = lane_id();
-    // one pass over the partials: the sums, and each lane keeps its
-    // sub-chunks' dp, fp and namb in LDS for the residual masses
+    // one pass over the partials, four per lane loaded together: the sums,
+    // and each lane keeps its sub-chunks' dp, fp and namb in LDS for the
+    // residual masses
     double st = 0.0, sq = 0.0;
-    for (int s = l; s < ns; s += 64) {
-      const NormPart P = np[s];
-      st += P.se;
-      sq += P.sf;
-      tsum[s] = P.dp;
-      s_fp[s] = P.fp;
-      s_na[s] = P.namb;
+    for (int s0 = l; s0 < ns; s0 += 4 * 64) {
+      if (s0 != l) load_parts(np, ns, s0, pse, psf, pdp, pfp, pna);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int s = s0 + 64 * j;
+        if (s < ns) {
+          st += pse[j];
+          sq += psf[j];
+          tsum[s] = pdp[j];
+          s_fp[s] = pfp[j];
+          s_na[s] = pna[j];
+        }
+      }
     }
     const double St = wave_reduce(st, OpAdd()), Sq = wave_reduce(sq, OpAdd());
     const double lam = St / Sq, lam0 = q.St / q.Sq;
