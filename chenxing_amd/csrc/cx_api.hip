@@ -270,8 +270,8 @@ static int verify_impl(const float* target, const float* draft, const int32_t* i
 // destructor could run after the HIP runtime has shut down.  Each arena has
 // its own stream (default priority), so a host call waits only for its own
 // copies and kernels.  The workspace part is zero-filled when it is
-// allocated, and every sampling or verify call leaves it zero-filled; a call
-// that fails after using it marks it for a refill.
+// allocated and again after a call that failed while using it (the kernels
+// need no initial contents there: each call writes what it reads first).
 //
 // Small calls (a decode step's rows) stage their inputs and outputs through a
 // pinned host mirror of the device part: the inputs are packed there with
@@ -366,12 +366,12 @@ class ArenaLease {
   // the pinned mirror of a device piece
   char* host(const void* dev_piece) const { return a_->host + ((const char*)dev_piece - a_->io); }
   void* ws() {
-    a_->ws_dirty = true;              // until finish() says the call left it zero-filled
+    a_->ws_dirty = true;              // until finish() says the call completed
     return a_->ws;
   }
   size_t ws_cap() const { return a_->ws_cap; }
   hipStream_t stream() const { return a_->stream; }
-  // the call completed: its kernels left the workspace zero-filled
+  // the call completed: no refill before the next call
   void finish() { a_->ws_dirty = false; }
 
  private:

@@ -76,9 +76,9 @@ typedef struct cx_row_params {
  *  row_status[B] int32 CX_ROW_* outcome | flags
  *  out_probs [B, V] fp32 post-filter normalised probabilities, or NULL.
  *            Costs one extra write of the batch; for verification.
- *  workspace device scratch of cx_sample_workspace_bytes(B, V, ldh) bytes,
- *            zero-filled once after allocation; the library leaves it
- *            zero-filled again after every call.  One workspace per stream.
+ *  workspace device scratch of cx_sample_workspace_bytes(B, V, ldh) bytes;
+ *            needs no initial contents (every call writes what it reads
+ *            there before reading it).  One workspace per stream.
  */
 int cx_sample_f32(const float* logits, int64_t ld, int32_t B, int32_t V,
                   const int32_t* hist, const int32_t* hist_len, int64_t ldh,
