@@ -220,11 +220,13 @@ __device__ __forceinline__ void deep_stream(const DeepRow& R, int lo, int stride
 
 // Does the row qualify, and its maximum M (from the fused kernel's slice
 // records: exact, the raw values being unpenalised).
-// (the conditions on the call and the row's parameters alone)
-__device__ inline bool deep_candidate(const SampleArgs& A, int row, const cx_row_params& P) {
+// (the conditions on the call and the row's parameters alone; a top-k
+// bound only where the caller's path applies it: the counted bf16 path)
+__device__ inline bool deep_candidate(const SampleArgs& A, int row, const cx_row_params& P,
+                                      bool topk_ok = false) {
   if (A.all_slow || A.out_probs) return false;
   if (!(P.temperature > 0.0) || P.typical_p < 1.0) return false;
-  if (P.top_k > 0 && P.top_k < A.V) return false;
+  if (P.top_k > 0 && P.top_k < A.V && !topk_ok) return false;
   if (A.logV * (1.0 / P.temperature) > 740.0) return false;       // P**(1/T) may underflow
   if (A.ldh > 0 && A.hist_len[row] > 0 &&
       (P.repetition_penalty != 1.0 || P.presence_penalty != 0.0 || P.frequency_penalty != 0.0))
@@ -232,8 +234,8 @@ __device__ inline bool deep_candidate(const SampleArgs& A, int row, const cx_row
   return true;
 }
 __device__ inline bool deep_eligible(const SampleArgs& A, int row, const cx_row_params& P,
-                                     double& M) {
-  if (!deep_candidate(A, row, P)) return false;
+                                     double& M, bool topk_ok = false) {
+  if (!deep_candidate(A, row, P, topk_ok)) return false;
   double m = -__builtin_inf();
   for (int s = 0; s < A.nsplit; ++s) {
     const double v = A.stats[(size_t)row * A.nsplit + s].m;

@@ -53,6 +53,8 @@ struct Deep16Shared {
   int we[NWAVE];
   double cut[3];                                  // v*'s term; the cut was robust; mass above its block
   int ci[4];                                      // cut block, kc, jk, token
+  int kq[2];                                      // top-k: the k-th largest's block, its key
+  double kqd[3];                                  // count and mass above that block; mass at or above the key
 };
 
 // Key of a bf16 code, ascending in the value (-0 folded onto +0, so equal
@@ -103,7 +105,7 @@ __device__ inline bool deep16_row_impl(const SampleArgs& A, int row, const cx_ro
   uint32_t* cw = (uint32_t*)dyn;
   for (int i = t; i < D16_WORDS; i += WG) cw[i] = 0u;
   for (int i = t; i < NWAVE * NWAVE; i += WG) { sh.gt[i] = 0.0; sh.eq[i] = 0; }
-  if (t == 0) { sh.ci[0] = INT_MAX; sh.cut[1] = 0.0; }
+  if (t == 0) { sh.ci[0] = INT_MAX; sh.cut[1] = 0.0; sh.kq[0] = -1; sh.kq[1] = 0; }
   load_exp64_tab(sh.tab);                            // its barrier also orders the clears
 
   // ---- pass 1: count every value (-inf, a masked token, in a register:
@@ -168,11 +170,55 @@ __device__ inline bool deep16_row_impl(const SampleArgs& A, int row, const cx_ro
     }
     kspan = lo;
   }
+  // top-k (sampler.py:76-79): every value at or above the k-th largest
+  // element's is kept, ties included.  kk is that value's key (0: no top-k
+  // bound, as when fewer than k values are finite).  Top-p then cuts the
+  // post-top-k vector, unrenormalised: where the mass at or above kk clearly
+  // falls short of top_p * S the whole top-k set is kept, otherwise the
+  // row's cut lies at or above kk, or it is handed back.
+  uint32_t kk = 0u;
+  bool topk_all = false;
+  if (P.top_k > 0 && P.top_k < V) {
+    int nb = 0;                                        // block t's count: its 32 counter words
+    const uint32_t* bw = cw + (32736 - 32 * t);
+    for (int i = 0; i < 32; ++i) nb += (int)((bw[i] & 0xFFFFu) + (bw[i] >> 16));
+    const double cbefore = block_excl_scan_d((double)nb, sh.s_d);
+    const double mbefore = block_excl_scan_d(c64, sh.s_d);
+    const double k = (double)P.top_k;
+    if (cbefore < k && cbefore + (double)nb >= k) {
+      sh.kq[0] = t;
+      sh.kqd[0] = cbefore;
+      sh.kqd[1] = mbefore;
+    }
+    __syncthreads();
+    const int kb = sh.kq[0];
+    if (kb >= 0) {
+      if (w == 0) {
+        // the block's keys in descending value: running counts and masses
+        const uint32_t key = 65535u - (uint32_t)(64 * kb + l);
+        const uint32_t n = d16_count(cw, key);
+        const double m = n ? (double)n * term(key) : 0.0;
+        double cin = (double)n, min_ = m;
+        for (int o = 1; o < 64; o <<= 1) {
+          const double yc = __shfl_up(cin, o), ym = __shfl_up(min_, o);
+          if (l >= o) { cin += yc; min_ += ym; }
+        }
+        const uint64_t hit = ballot(sh.kqd[0] + cin >= k);
+        if (hit && l == __builtin_ctzll(hit)) {
+          sh.kq[1] = (int)key;
+          sh.kqd[2] = sh.kqd[1] + min_;
+        }
+      }
+      __syncthreads();
+      kk = (uint32_t)sh.kq[1];
+      topk_all = !(P.top_p < 1.0) || sh.kqd[2] < P.top_p * S - DTOL * S;
+    }
+  }
   // kept: key > kc, or key == kc among its first jk occurrences in id order
   uint32_t kc = kspan - 1;
   int jk = 0;
   double termc = 0.0;
-  if (P.top_p < 1.0) {
+  if (P.top_p < 1.0 && !topk_all) {
     const double tgt = P.top_p * S;
     const double tolS = DTOL * S;
     const double before = block_excl_scan_d(c64, sh.s_d);
@@ -216,6 +262,7 @@ __device__ inline bool deep16_row_impl(const SampleArgs& A, int row, const cx_ro
     jk = sh.ci[2];
     termc = sh.cut[0];
   }
+  if (kc < kk) { kc = kk - 1; jk = 0; termc = 0.0; }   // the top-k bound
   if (P.min_p > 0.0) {
     // the lowest key whose term reaches min_p (the top term is 1)
     const double minp = P.min_p, mtol = 1e-12 * minp;
@@ -454,7 +501,7 @@ __device__ inline bool deep16_row(const SampleArgs& A, int row, unsigned char* d
   if (!A.bf16) return false;
   const cx_row_params P = A.prm[row];
   double M = 0.0;
-  if (!deep_eligible(A, row, P, M)) return false;
+  if (!deep_eligible(A, row, P, M, true)) return false;   // (top-k rows too)
   return A.vec_ok ? deep16_row_impl<true>(A, row, P, M, dyn, red_d, red_i, sh)
                   : deep16_row_impl<false>(A, row, P, M, dyn, red_d, red_i, sh);
 }

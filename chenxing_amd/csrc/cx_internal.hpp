@@ -34,8 +34,10 @@ constexpr int ROW_PENDING = 0x40000000;
 constexpr int ROW_REFINE = 0x40000001;
 constexpr int ROW_FINISH = 0x40000002;
 // In a single-slice row's hand-off mark (SampleArgs::counters), beside its
-// ROW_* value: the row may take a deep-nucleus path (deep_candidate).
+// ROW_* value: the row may take the counted deep-nucleus path
+// (deep_candidate, top-k allowed), and it has a top-k bound.
 constexpr int MARK_DEEP = 0x00010000;
+constexpr int MARK_TOPK = 0x00020000;
 
 struct SplitStats {       // one per (row, slice), 64 bytes
   double m;               // max of the slice's penalised values (stochastic rows)
@@ -73,9 +75,9 @@ struct SampleArgs {
   // [B + 1], each written by the fused kernel before the later kernels read
   // it: [row] of a sliced row, its exact-normaliser shares summed (zeroed);
   // [row] of a single-slice row, its hand-off mark (ROW_FINISH, ROW_REFINE,
-  // ROW_PENDING, or 0 if decided, with MARK_DEEP), which, unlike row_status,
-  // the finishing kernels leave as it is; [B], finish16_kernel's work-item
-  // counter (zeroed)
+  // ROW_PENDING, or 0 if decided, with MARK_DEEP and MARK_TOPK), which,
+  // unlike row_status, the finishing kernels leave as it is; [B],
+  // finish16_kernel's work-item counter (zeroed)
   int32_t* counters;
   SplitStats* stats;      // [B * nsplit]
   Cand* cands;            // [B * nsplit * CAPS]

@@ -1068,8 +1068,13 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   // (finish16_kernel counts its values from its maximum on, and decides it
   // exactly or hands it to the exact path) needs only its maximum here: the
   // greedy stream, with no region.  (Its region would be a candidate list
-  // its nucleus usually outgrows.)
-  const bool count_row = BF16 && single && !greedy && !A.out_probs && deep_candidate(A, row, P);
+  // its nucleus usually outgrows, or, for top-k above 256, one whose upkeep
+  // here, ~50 us a row, costs about what counting the row there does.)
+  // Top-k rows up to 64 keep the one-wave finish below, those up to 256 the
+  // region finisher.  (Counting every top-k row above 64 left the counting
+  // kernel three rounds of workgroups deep: 400 instead of 337 us.)
+  const bool count_row = BF16 && single && !greedy && !A.out_probs &&
+                         !(P.top_k > 0 && P.top_k <= 256) && deep_candidate(A, row, P, true);
   // ---------------------------------------------------------------- greedy
   if (greedy || count_row) {
     GreedyState gs{-__builtin_inff(), INT_MAX, INT_MAX};
@@ -1098,7 +1103,7 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
         my->tau = 1u; my->ncand = 0; my->flags = 0;
         A.out_id[row] = -1;
         A.row_status[row] = ROW_PENDING;
-        A.counters[row] = ROW_PENDING | MARK_DEEP;
+        A.counters[row] = ROW_PENDING | MARK_DEEP | (P.top_k > 0 && P.top_k < A.V ? MARK_TOPK : 0);
       }
     } else if (single) {
       const int tok = ni != INT_MAX ? ni : (bi == INT_MAX ? 0 : bi);
@@ -1287,7 +1292,7 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
       const int mark = dr == LEAN_DONE ? 0 : (dr == LEAN_NEAR ? ROW_REFINE : ROW_PENDING);
       A.out_id[row] = dr == LEAN_DONE ? tok : -1;
       A.row_status[row] = mark ? mark : CX_ROW_OK;
-      A.counters[row] = mark | (mark && deep_candidate(A, row, P) ? MARK_DEEP : 0);
+      A.counters[row] = mark | (mark && deep_candidate(A, row, P, true) ? MARK_DEEP | MARK_TOPK : 0);
     }
     return;
   }
@@ -1372,6 +1377,8 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   // is marked.
   if (single && t == 0) {
     A.row_status[row] = ROW_FINISH;
+    // (a top-k row here has a small region: its finisher, not counting, is
+    // what it usually needs, so it goes with the rows that cannot go deep)
     A.counters[row] = ROW_FINISH | (deep_candidate(A, row, P) ? MARK_DEEP : 0);
   }
 }

@@ -144,27 +144,36 @@ __global__ __launch_bounds__(WG) void slow_kernel(SampleArgs A) {
   slow_row(A, row, dyn, red_d, red_i);
 }
 
-// finish16_kernel's work items: 0 for a row with nothing left to do, 1 for
-// a row that may go deep (the long ones), 2 for another row with work.  From
-// the fused kernel's hand-off marks (one load), which nothing changes during
-// the kernel; a sliced row's are all finished, the deep test from its
+// finish16_kernel's work items, in the order they are taken: 1 for a row
+// that may go deep without a top-k bound (the ones that can be long), 2 for
+// one with a top-k bound (counted, its kept set near the top), 3 for
+// another row with work; 0 for a row with nothing left to do.  From the
+// fused kernel's hand-off marks (one load), which nothing changes during
+// the kernel; a sliced row's are all finished, its class from its
 // parameters.  A pending row that cannot go deep is left to slow_kernel as
 // it is.
 __device__ inline int f16_class(const SampleArgs& A, int row) {
-  const int m = A.nsplit > 1 ? (ROW_FINISH | (deep_candidate(A, row, A.prm[row]) ? MARK_DEEP : 0))
-                             : A.counters[row];
-  const int mark = m & ~MARK_DEEP;
-  const bool deep = (m & MARK_DEEP) != 0;
-  if (mark == ROW_FINISH || mark == ROW_REFINE) return deep ? 1 : 2;
-  return mark == ROW_PENDING && deep ? 1 : 0;
+  int m;
+  if (A.nsplit > 1) {
+    const cx_row_params& P = A.prm[row];
+    m = ROW_FINISH | (deep_candidate(A, row, P, true) ? MARK_DEEP : 0) |
+        (P.top_k > 0 && P.top_k < A.V ? MARK_TOPK : 0);
+  } else {
+    m = A.counters[row];
+  }
+  const int mark = m & ~(MARK_DEEP | MARK_TOPK);
+  const int deep = !(m & MARK_DEEP) ? 3 : (m & MARK_TOPK) ? 2 : 1;
+  if (mark == ROW_FINISH || mark == ROW_REFINE) return deep;
+  return mark == ROW_PENDING && deep != 3 ? deep : 0;
 }
 
 // The row of item idx of finish16_kernel's list: the class-1 rows in row
-// order, then the class-2 rows (nd of class 1).  Every thread gets it.
-// cnt: NWAVE ints; out: one int.
-__device__ inline int f16_item_row(const SampleArgs& A, int idx, int nd, int* cnt, int* out) {
-  const int want = idx < nd ? 1 : 2;
-  const int target = idx < nd ? idx : idx - nd;
+// order (n1 of them), then the class-2 rows (n2), then the class-3 rows.
+// Every thread gets it.  cnt: NWAVE ints; out: one int.
+__device__ inline int f16_item_row(const SampleArgs& A, int idx, int n1, int n2, int* cnt,
+                                   int* out) {
+  const int want = idx < n1 ? 1 : idx < n1 + n2 ? 2 : 3;
+  const int target = idx < n1 ? idx : idx < n1 + n2 ? idx - n1 : idx - n1 - n2;
   const int t = threadIdx.x, w = wave_id();
   int base = 0;                                   // items of that class in earlier chunks
   if (t == 0) *out = -1;                          // (ordered by the loop's first barrier)
@@ -207,19 +216,21 @@ __global__ __launch_bounds__(WG) void finish16_kernel(SampleArgs A) {
   enum { OPEN, REFINE, FINISH };
   const int t = threadIdx.x;
   if (t == 0) s_item[0] = atomicAdd(A.counters + A.B, 1);
-  int nd = 0, nw = 0;
+  int n1 = 0, n2 = 0, nw = 0;
   for (int c = 0; c < A.B; c += WG) {
     const int cls = c + t < A.B ? f16_class(A, c + t) : 0;
-    nd += cls == 1;
+    n1 += cls == 1;
+    n2 += cls == 2;
     nw += cls != 0;
   }
-  nd = block_sum(nd, red_i);                      // (its barriers also publish s_item[0])
+  n1 = block_sum(n1, red_i);                      // (its barriers also publish s_item[0])
+  n2 = block_sum(n2, red_i);
   nw = block_sum(nw, red_i);
   const int idx = s_item[0];
   if (idx >= nw) return;
-  const int row = f16_item_row(A, idx, nd, red_i, s_item + 1);
+  const int row = f16_item_row(A, idx, n1, n2, red_i, s_item + 1);
   if (row < 0) return;                            // (every workgroup's list is the same)
-  const int mark = A.nsplit > 1 ? ROW_FINISH : A.counters[row] & ~MARK_DEEP;
+  const int mark = A.nsplit > 1 ? ROW_FINISH : A.counters[row] & ~(MARK_DEEP | MARK_TOPK);
   int state = mark == ROW_FINISH ? FINISH : mark == ROW_REFINE ? REFINE : OPEN;
   if (state == FINISH) {
     const cx_row_params P = A.prm[row];

@@ -162,3 +162,30 @@ def test_counted_deep_path_emulated_on_bf16_rows():
            RowParams(temperature=1.0, top_p=0.9)]
     groups.append(("bf16", xb, prm, {2}, None))
     assert _run(groups, 16) == 11 + 2
+
+
+def test_counted_deep_path_top_k_rows():
+    """deep16_row on bf16 rows with a top-k bound (sampler.py:76-79: every
+    value at or above the k-th largest kept, ties included), alone and with
+    top-p cutting inside the top-k set or beyond it (then the whole set is
+    kept), with min-p, with ties at the k-th value and with k above the
+    number of finite values: every row sampled as the oracle samples it."""
+    rng = np.random.default_rng(17)
+    V = 40000
+    xb = f32_to_bf16_rne(rng.normal(0, 2.0, (10, V)).astype(np.float32))
+    xb[3, :] = f32_to_bf16_rne(np.round(rng.normal(0, 2.0, V) * 4).astype(np.float32) / 4)
+    xb[9, rng.choice(V, V - 50, replace=False)] = 0xFF80          # 50 finite values
+    prm = [RowParams(temperature=1.0, top_k=100),
+           RowParams(temperature=0.8, top_k=1000, top_p=0.9),
+           RowParams(temperature=1.2, top_k=1000, top_p=0.3),
+           RowParams(temperature=1.0, top_k=77, top_p=0.95),        # ties at the k-th value
+           RowParams(temperature=1.5, top_k=5000, top_p=0.99),
+           RowParams(temperature=1.0, top_k=300, min_p=0.05),
+           RowParams(temperature=2.0, top_k=2000, top_p=0.8, min_p=0.01),
+           RowParams(temperature=0.7, top_k=65),
+           RowParams(temperature=1.0, top_k=20000, top_p=0.97),
+           RowParams(temperature=1.0, top_k=100, top_p=0.9)]
+    rows = bf16_to_f32(xb)
+    kth = np.sort(rows[3])[::-1][76]
+    assert np.sum(rows[3] == kth) > 1 and np.sum(rows[3] > kth) < 77      # a tie at the k-th
+    assert _run([("bf16", xb, prm, set(), None)], 16) == 10
