@@ -15,6 +15,10 @@
 //           number j of its occurrences kept, equal values keeping the
 //           lower ids first (sampler.py:81-89, stable order of equal
 //           probabilities)
+//   top-k   the k-th largest element's value from the counts, every value
+//           at or above it kept (sampler.py:76-79, ties included); top-p
+//           cuts that set unrenormalised, so where its mass falls short of
+//           top_p * S the whole set is kept
 //   min-p   kept values are those whose term reaches min_p times the top
 //           term, 1 (sampler.py:91-93)
 //   ranges  per range, the kept mass above v* and the number of v*'s
