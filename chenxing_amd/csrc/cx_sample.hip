@@ -196,6 +196,19 @@ __device__ __forceinline__ int next_chunk(CX_LDS int* counter) {
 // step, three independent ballot counts each.  Inlined: a call makes the
 // callee wait for every load in flight (the calling convention), which in
 // the stream would drain the wave's chunk pipeline.
+// The k-th largest of the wave's 128 values v1, v2 (two per lane), as
+// kth_of_lanes.
+__device__ __forceinline__ uint32_t kth_of_lanes2(uint32_t v1, uint32_t v2, int k) {
+  uint32_t prefix = 0u;
+  for (int sh = 30; sh >= 0; sh -= 2) {
+    const uint32_t b1 = prefix | (1u << sh), b2 = prefix | (2u << sh), b3 = prefix | (3u << sh);
+    const int c3 = __popcll(ballot(v1 >= b3)) + __popcll(ballot(v2 >= b3));
+    const int c2 = __popcll(ballot(v1 >= b2)) + __popcll(ballot(v2 >= b2));
+    const int c1 = __popcll(ballot(v1 >= b1)) + __popcll(ballot(v2 >= b1));
+    prefix = c3 >= k ? b3 : (c2 >= k ? b2 : (c1 >= k ? b1 : prefix));
+  }
+  return prefix;
+}
 __device__ __forceinline__ uint32_t kth_of_lanes(uint32_t v, int k) {
   uint32_t prefix = 0u;
   for (int sh = 30; sh >= 0; sh -= 2) {
@@ -1161,15 +1174,37 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   }
   // The waves' first chunks together set the first threshold: for top-k
   // rows (k <= 64) the k-th largest of the published lane values, for wider
-  // rows the smallest of the waves' r-th largest lane values.  (A wave's own
-  // lane values alone give a threshold too low to keep the first chunks'
-  // appends cheap.)
+  // rows the smallest of the waves' r-th largest of their lanes' two largest
+  // values (every one an element, so each wave holds r elements at or
+  // above it).  (A wave's own lane values alone give a threshold too low to
+  // keep the first chunks' appends cheap, and with r = 64 the lane maxima
+  // alone give their smallest.)
   if (krow <= 64) {
     publish_top(ck, NSLOT, lslots + NSLOT * wave_id());
     __syncthreads();
     raise_tau(wb, kth_of_lanes(lds_load(lslots + lane_id()), krow));
   } else if (pub_r > 0) {
-    const uint32_t th = kth_of_lanes(ck, pub_r);
+    // for r of 32 and more, the lanes' second largest values of the same
+    // chunk too (for smaller r the r-th largest lane maximum is already
+    // high, and the extra pass costs more than it saves)
+    uint32_t c1 = 0u, c2 = 0u;
+    if (pub_r >= 32 && wave_id() * CH < nv) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int vi = wave_id() * CH + u * 64 + lane_id();
+        float x[NE];
+        E::unpack(q[u], x);
+        const uint32_t pb = pen_bits<NE>(X, pen_on && vi < nv, vi * NE);
+#pragma unroll
+        for (int j = 0; j < NE; ++j) {
+          const bool ok = vi < nv && x[j] == x[j] && !((pb >> j) & 1u);
+          const uint32_t k = ok ? f2key(x[j]) : 0u;
+          c2 = k > c1 ? c1 : (k > c2 ? k : c2);
+          c1 = k > c1 ? k : c1;
+        }
+      }
+    }
+    const uint32_t th = pub_r >= 32 ? kth_of_lanes2(c1, c2, pub_r) : kth_of_lanes(ck, pub_r);
     if (lane_id() == 0) lpub[wave_id()] = th;
     __syncthreads();
     raise_tau(wb, pub_min(lpub));
