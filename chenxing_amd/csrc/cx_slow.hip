@@ -202,11 +202,12 @@ __device__ inline int f16_item_row(const SampleArgs& A, int idx, int n1, int n2,
 // multi-pass path: slow_kernel's register allocation stays as it is, and a
 // deep-nucleus row starts counting right after its finisher gives up.)
 // Grid B: each workgroup takes the next work item from a counter, in the
-// order the workgroups start, so the rows that may go deep (the long ones)
-// start together on the first workgroups, the others follow on the CUs as
-// they free up, and the workgroups left without an item exit last.  (With
-// one workgroup per row and kind, blockIdx order, some deep rows started
-// 40 us late, behind workgroups that only read a status word and exit.)
+// order the workgroups start (f16_class: the rows that may be long, then the
+// counted top-k rows, then the finisher rows), so the long rows start
+// together on the first workgroups, the others follow on the CUs as they
+// free up, and the workgroups left without an item exit last.  (With one
+// workgroup per row and kind, blockIdx order, some deep rows started 40 us
+// late, behind workgroups that only read a status word and exit.)
 __global__ __launch_bounds__(WG) void finish16_kernel(SampleArgs A) {
   extern __shared__ __align__(16) unsigned char dyn[];
   __shared__ double red_d[2 * NWAVE + 4];
