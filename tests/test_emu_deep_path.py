@@ -189,3 +189,28 @@ def test_counted_deep_path_top_k_rows():
     kth = np.sort(rows[3])[::-1][76]
     assert np.sum(rows[3] == kth) > 1 and np.sum(rows[3] > kth) < 77      # a tie at the k-th
     assert _run([("bf16", xb, prm, set(), None)], 16) == 10
+
+
+def test_counted_deep_path_kept_range_through_zero():
+    """deep16_row on kept ranges through zero, whose ~27K codes of values
+    below 2^-20 in magnitude outgrow a term table by key (the three part
+    tables of every bf16 code): rows of logits with such values and signed
+    zeros kept, and a row of only tiny values: every row sampled as the
+    oracle samples it."""
+    rng = np.random.default_rng(23)
+    V = 40000
+    x = rng.normal(0, 2.0, (4, V)).astype(np.float32)
+    for b in range(3):
+        idx = rng.choice(V, 200, replace=False)
+        x[b, idx[:60]] = rng.normal(0, 1e-7, 60).astype(np.float32)      # inside the gap
+        x[b, idx[60:80]] = np.float32(0.0)
+        x[b, idx[80:100]] = np.float32(-0.0)
+        x[b, idx[100:]] = rng.normal(0, 1e-5, 100).astype(np.float32)    # just outside it
+    x[3] = rng.normal(0, 1.0, V).astype(np.float32) * np.float32(1e-8)   # only tiny values
+    xb = f32_to_bf16_rne(x)
+    prm = [RowParams(temperature=2.0, top_p=0.95), RowParams(temperature=1.5, top_p=0.99),
+           RowParams(temperature=3.0, top_p=0.9, min_p=0.001), RowParams(temperature=1.0, top_p=0.9)]
+    rows = bf16_to_f32(xb)
+    tiny = np.abs(rows) < 2.0 ** -20
+    assert tiny[:3].sum(axis=1).min() >= 60 and tiny[3].all()
+    assert _run([("bf16", xb, prm, set(), None)], 16) == 4
