@@ -78,3 +78,29 @@ def test_counted_bf16_rows_and_hand_backs():
                      ref_rows=[p[1] for p in pairs])
     assert not t.mismatches, t.mismatches[:5]
     assert t.draws == B and t.boundary == 0
+
+
+def test_counted_rows_in_a_batch_beyond_one_workgroup():
+    """A bf16 batch of 1100 single-slice rows (more rows than a workgroup
+    has threads, so finish16_kernel's work list is built over two chunks of
+    rows), mixing greedy rows, top-k 20 rows (one-wave finish), top-k 100
+    rows (regions and the finisher), and top-k 1000 and top-p-only rows
+    (streamed for their maximum only, then counted): every row sampled as
+    the oracle samples it."""
+    rng = np.random.default_rng(91)
+    B, V = 1100, 16384
+    x = rng.normal(0, 2.0, (B, V)).astype(np.float32)
+    x[np.arange(B), rng.integers(0, V, B)] += np.float32(6.0)
+    kinds = [dict(temperature=0.0), dict(temperature=0.8, top_k=20, top_p=0.9),
+             dict(temperature=1.0, top_k=100, top_p=0.95), dict(temperature=1.1, top_k=1000, top_p=0.9),
+             dict(temperature=1.3, top_p=0.9), dict(temperature=0.9, top_p=0.97, min_p=0.01)]
+    prm = [RowParams(**kinds[int(k)]) for k in rng.integers(0, len(kinds), B)]
+    w = W.SampleWorkload("counted_mixed", W.f32_to_bf16_rne(x), "bf16", prm,
+                         np.zeros((B, 0), np.int32), np.zeros(B, np.int32), rng.random(B))
+    print(f"[gpu] counted rows in a mixed bf16 batch B={B} V={V}", flush=True)
+    ids, st, _ = sample_host(w.logits, w.params, None, None, w.u, bf16=True)
+    pairs = oracle_rows_parallel(w, ties=("stable", "numpy"))
+    t = compare_rows(ids, st, None, [p[0] for p in pairs], "counted_mixed[B=1100]",
+                     ref_rows=[p[1] for p in pairs])
+    assert not t.mismatches, t.mismatches[:5]
+    assert t.boundary == 0
