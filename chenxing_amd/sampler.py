@@ -35,9 +35,17 @@ from .params import RowParams, SamplingParams, pack_rows
 
 __all__ = ["Sampler", "SamplingParams"]
 
-# Longest penalty window the device holds (distinct ids when only the
-# repetition and presence penalties are on).
+# Longest penalty window one launch of the device's penalty index holds
+# (distinct ids when only the repetition and presence penalties are on).
 WINDOW_MAX = 4095
+
+
+class _Groups(list):
+    """A penalty window longer than WINDOW_MAX, as groups of at most
+    WINDOW_MAX ids with disjoint id sets (every occurrence of an id in one
+    group).  The penalties act on each id alone, from its value and its count
+    (sampler.py:70-72), so applying the groups one after another gives the
+    row that one pass over the whole window would."""
 
 _NUMPY_NAN = "probabilities contain NaN"          # numpy Generator.choice's message
 _NUMPY_SIZE = "'a' and 'p' must have same size"
@@ -92,15 +100,41 @@ class Sampler:
                                  f"with size {V}")
         h = np.where((h >= 0) & (h < min(V, self.vocab_size)), h, -1)
         if h.size > WINDOW_MAX:
-            if freq != 0.0:
-                raise ValueError(f"frequency penalty over a window of {h.size} ids: the "
-                                 f"device holds at most {WINDOW_MAX}")
+            h = h[h >= 0]
+        if h.size <= WINDOW_MAX:
+            return h.astype(np.int32)
+        ids, cnt = np.unique(h, return_counts=True)
+        if freq == 0.0:
             # repetition and presence penalties depend on the set of ids only
-            h = np.unique(h[h >= 0])
-            if h.size > WINDOW_MAX:
-                raise ValueError(f"penalty window holds {h.size} distinct ids: the device "
-                                 f"holds at most {WINDOW_MAX}")
-        return h.astype(np.int32)
+            if ids.size <= WINDOW_MAX:
+                return ids.astype(np.int32)
+            return _Groups(ids[i:i + WINDOW_MAX].astype(np.int32)
+                           for i in range(0, ids.size, WINDOW_MAX))
+        if int(cnt.max()) > WINDOW_MAX:
+            raise ValueError(f"frequency penalty over an id seen {int(cnt.max())} times in "
+                             f"the window: the device counts at most {WINDOW_MAX}")
+        # the ids with their counts, packed in id order into groups of at
+        # most WINDOW_MAX occurrences
+        groups, start, n = _Groups(), 0, 0
+        for i, c in enumerate(cnt.tolist()):
+            if n + c > WINDOW_MAX:
+                groups.append(np.repeat(ids[start:i], cnt[start:i]).astype(np.int32))
+                start, n = i, 0
+            n += c
+        groups.append(np.repeat(ids[start:], cnt[start:]).astype(np.int32))
+        return groups
+
+    @staticmethod
+    def _penalise_groups(row, bf16: bool, params, groups: _Groups) -> np.ndarray:
+        """The fp64 row with a long window's penalties applied, group by
+        group, on the device (one apply_penalties launch per group)."""
+        prm = [RowParams.of(params)]
+        out = np.asarray(row)[None]
+        for k, g in enumerate(groups):
+            out, st = _lib.apply_penalties_host(out, prm, g[None], bf16=bf16 and k == 0)
+            if st[0] != _lib.ROW_OK:
+                raise ValueError(f"apply_penalties: device status {int(st[0])}")
+        return out[0]
 
     @staticmethod
     def _as_row(logits) -> tuple[np.ndarray, bool]:
@@ -117,6 +151,8 @@ class Sampler:
         """fp64 copy of the row with the penalties applied (sampler.py:63-73)."""
         x, _ = self._as_row(logits)
         win = self._window(params, generated_ids, x.size)
+        if isinstance(win, _Groups):
+            return self._penalise_groups(x, False, params, win)
         hist = None if win is None else win[None]
         out, st = _lib.apply_penalties_host(x[None], [RowParams.of(params)], hist)
         if st[0] != _lib.ROW_OK:
@@ -176,6 +212,28 @@ class Sampler:
         if B == 0:
             return []
         wins = [self._window(p, h or [], V) for p, h in zip(plist, hists)]
+        # rows whose window one launch cannot hold: their penalised fp64 rows
+        # (group by group), sampled with the penalties off on the exact fp64
+        # path; the other rows take the batch launch
+        longs = [b for b, w in enumerate(wins) if isinstance(w, _Groups)]
+        pen = prm_long = None
+        if longs:
+            rows_l = []
+            for b in longs:
+                if on_dev:
+                    r = logits[b]
+                    bf = r.dtype == torch.bfloat16
+                    r = (r.view(torch.int16).cpu().numpy().view(np.uint16) if bf
+                         else r.cpu().numpy())
+                else:
+                    r, bf = x[b], False
+                rows_l.append(self._penalise_groups(r, bf, plist[b], wins[b]))
+                wins[b] = None
+            pen = np.stack(rows_l)
+            prm_long = pack_rows([plist[b] for b in longs])
+            for f in ("presence_penalty", "frequency_penalty"):
+                prm_long[f] = 0.0
+            prm_long["repetition_penalty"] = 1.0
         H = max((w.size for w in wins if w is not None), default=0)
         hist = hist_len = None
         if H > 0:
@@ -191,6 +249,23 @@ class Sampler:
 
         def run(u, rows=None):
             """Sample every row, or the listed rows only (returned in that order)."""
+            if not longs:
+                return run_batch(u, rows)
+            sel = list(range(B)) if rows is None else list(rows)
+            at = {b: i for i, b in enumerate(longs)}
+            ids = np.empty(len(sel), np.int32)
+            st = np.empty(len(sel), np.int32)
+            ia = [i for i, b in enumerate(sel) if b not in at]
+            il = [i for i, b in enumerate(sel) if b in at]
+            if ia:
+                ids[ia], st[ia] = run_batch(u, [sel[i] for i in ia])
+            if il:
+                li = [at[sel[i]] for i in il]
+                ids[il], st[il], _ = _lib.sample_host(pen[li], prm_long[li], None, None,
+                                                      u[[sel[i] for i in il]])
+            return ids, st
+
+        def run_batch(u, rows=None):
             sel = slice(None) if rows is None else rows
             h = None if hist is None else hist[sel]
             hl = None if hist_len is None else hist_len[sel]

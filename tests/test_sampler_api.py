@@ -6,6 +6,7 @@ import numpy as np
 import pytest
 
 from chenxing_amd import Sampler, SamplingParams
+from chenxing_amd.sampler import WINDOW_MAX, _Groups
 
 
 def test_invalid_params_raise():                       # chenxing tests/test_sampler.py:64-69
@@ -49,11 +50,48 @@ def test_long_window_deduplicated_when_counts_do_not_matter():
     h = [i % 50 for i in range(10_000)]
     w = s._window(SamplingParams(repetition_penalty=1.1, presence_penalty=0.2), h, 100)
     assert sorted(w.tolist()) == list(range(50))
+
+
+def _check_groups(groups, window, counted):
+    """Disjoint id sets, at most 4095 ids each, together the window's ids
+    (with their multiplicities when counted)."""
+    assert isinstance(groups, _Groups) and len(groups) > 1
+    seen = set()
+    for g in groups:
+        assert g.dtype == np.int32 and 0 < g.size <= WINDOW_MAX
+        ids = set(g.tolist())
+        assert not ids & seen
+        seen |= ids
+        if not counted:
+            assert len(ids) == g.size
+    w = np.asarray([t for t in window if t >= 0])
+    if counted:
+        assert np.array_equal(np.sort(np.concatenate(groups)), np.sort(w))
+    else:
+        assert seen == set(w.tolist())
+
+
+def test_long_windows_split_into_groups():
+    """Windows the device index cannot hold in one launch: groups of ids
+    applied one after another (each id's penalty depends on its own value
+    and count only)."""
+    h = [i % 50 for i in range(10_000)]
+    _check_groups(Sampler(100)._window(SamplingParams(frequency_penalty=0.1), h, 100), h,
+                  True)
+    h = list(range(5000)) + [-3, 10**6]
+    _check_groups(Sampler(10_000)._window(SamplingParams(repetition_penalty=1.1), h, 10_000),
+                  [t if t < 10_000 else -1 for t in h], False)
+    rng = np.random.default_rng(3)
+    h = rng.integers(0, 20_000, 12_000).tolist()
+    _check_groups(Sampler(20_000)._window(SamplingParams(frequency_penalty=0.3,
+                                                         presence_penalty=0.1), h, 20_000),
+                  h, True)
+    # out-of-range ids leave a window that fits: one plain window
+    w = Sampler(100)._window(SamplingParams(frequency_penalty=0.1), [5] * 100 + [-1] * 5000, 100)
+    assert not isinstance(w, _Groups) and w.tolist() == [5] * 100
+    # one id counted more often than one launch can count
     with pytest.raises(ValueError):
-        s._window(SamplingParams(frequency_penalty=0.1), h, 100)
-    with pytest.raises(ValueError):
-        Sampler(10_000)._window(SamplingParams(repetition_penalty=1.1), list(range(5000)),
-                                10_000)
+        Sampler(100)._window(SamplingParams(frequency_penalty=0.1), [7] * 5000, 100)
 
 
 def test_batch_argument_checks():
