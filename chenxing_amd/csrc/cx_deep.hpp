@@ -20,8 +20,9 @@
 //           top_p * S (sampler.py:82-85: cumsum of the sorted
 //           probabilities, searchsorted, one past the index)
 //   pass 2  the elements of that bucket, gathered, sorted by value
-//           (descending) and id (ascending: equal probabilities keep the
-//           lower id first) and scanned: the cut element.  The same pass
+//           (descending) and id (ascending) and scanned: the cut element;
+//           of the cut value's group the survivors spread over its ids
+//           (spread_kept, cx_device.hpp).  The same pass
 //           adds, per range, the terms of the cut's coarse bucket that lie
 //           above the cut bucket, so each range's kept mass follows from the
 //           copies.  (With min-p, pass 3 instead sums each range's kept terms
@@ -246,13 +247,14 @@ __device__ inline bool deep_eligible(const SampleArgs& A, int row, const cx_row_
 }
 
 template <bool VEC>
-__device__ inline bool deep_row_impl(const SampleArgs& A, int row, const cx_row_params& P,
+__device__ __forceinline__ bool deep_row_impl(const SampleArgs& A, int row, const cx_row_params& P,
                                      double M, unsigned char* dyn, double* red_d, int* red_i) {
   __shared__ double tab[64];
   __shared__ double s_d[2 * NWAVE + 4];
   __shared__ double s_wm[NWAVE];                     // kept mass per wave range / sixteenth
   __shared__ unsigned long long s_corr[2 * NWAVE];   // per range: cut coarse bucket, cut bucket
   __shared__ int s_i[4];
+  __shared__ int s_g[2];
   const int t = threadIdx.x, l = lane_id(), w = wave_id();
   DeepRow R;
   R.V = A.V;
@@ -327,7 +329,7 @@ __device__ inline bool deep_row_impl(const SampleArgs& A, int row, const cx_row_
   // ---- the cut: first non-empty bucket whose inclusive sum reaches top_p * S
   const bool cut = P.top_p < 1.0;
   float xcut = -__builtin_inff();
-  int idcut = INT_MAX;
+  int g0 = 0, gn = 0, gj = 0;                        // the cut value's group: none
   int bs = DNB;                                      // no cut: every bucket above it
   if (cut) {
     const double tgt = P.top_p * S;
@@ -430,31 +432,58 @@ __device__ inline bool deep_row_impl(const SampleArgs& A, int row, const cx_row_
       const bool first = bs == 0 && js == 0;
       const bool ok = cstar >= tgt + tolS && (first || cprev < tgt - tolS);
       s_i[1] = ok ? 1 : 0;
-      s_i[2] = gi[js];
+      s_g[0] = js;
+      s_g[1] = js + 1;
       red_d[2 * NWAVE + 2] = key2d(gk[js]);
     }
     __syncthreads();
     if (!s_i[1]) return false;
+    // the cut value's group: sorted positions [g0, g1), ascending ids
+    {
+      const uint64_t kj = gk[js];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int e = 4 * t + j;
+        if (e < ng && gk[e] == kj) { atomicMin(&s_g[0], e); atomicMax(&s_g[1], e + 1); }
+      }
+    }
+    __syncthreads();
     xcut = (float)red_d[2 * NWAVE + 2];
-    idcut = s_i[2];
-    // the kept part of the cut bucket, per range
+    g0 = s_g[0];
+    gn = s_g[1] - g0;
+    gj = js + 1 - g0;
+    // the kept part of the cut bucket, per range: the entries above the cut
+    // value and the group's survivors
     if (corr) {
       const double fb = deep_pow2(deep_scale(bs));
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int e = 4 * t + j;
-        if (e <= js) atomicAdd(s_corr + NWAVE + gi[e] / L, (unsigned long long)(qv[j] * fb));
+        if (e < g0 || (e < g0 + gn && spread_keeps(e - g0, gj, gn)))
+          atomicAdd(s_corr + NWAVE + gi[e] / L, (unsigned long long)(qv[j] * fb));
       }
     }
     __syncthreads();
   }
 
-  // kept: above the cut value, or at it with an id up to the cut element's;
+  // kept: above the cut value, or in its group among the survivors (the
+  // group's member of a given id found by bisection of its sorted ids);
   // with min-p, e >= min_p
   const double minp = P.min_p;
   const double minp_tol = 1e-12 * minp;
+  const uint32_t kcut = f2key(xcut);
+  auto in_group = [&](int id) -> bool {
+    if (gj >= gn) return true;
+    int lo = g0, hi = g0 + gn;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (gi[mid] < id) lo = mid + 1; else hi = mid;
+    }
+    return spread_keeps(lo - g0, gj, gn);
+  };
   auto kept_e = [&](float x, int id, int& amb) -> double {
-    if (!(x > xcut || (x == xcut && id <= idcut))) return 0.0;
+    const uint32_t kx = f2key(x);
+    if (!(kx > kcut || (kx == kcut && in_group(id)))) return 0.0;
     const double ev = deep_term(x, M, invT, tab);
     if (minp > 0.0) {
       if (fabs(ev - minp) <= minp_tol) amb = 1;
@@ -638,7 +667,7 @@ __device__ inline double deep_exact_sum(const SampleArgs& A, int row, double M, 
 // (the caller runs the multi-pass path).  All threads of the workgroup call
 // it and get the same result.  dyn: DEEP_LDS bytes; red_d, red_i: >= 2 *
 // NWAVE + 4 slots.
-__device__ inline bool deep_row(const SampleArgs& A, int row, unsigned char* dyn, double* red_d,
+__device__ __forceinline__ bool deep_row(const SampleArgs& A, int row, unsigned char* dyn, double* red_d,
                                 int* red_i) {
   const cx_row_params P = A.prm[row];
   double M = 0.0;

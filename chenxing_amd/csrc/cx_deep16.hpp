@@ -12,9 +12,8 @@
 //           bucket span below M; terms below it are left out, at most
 //           V exp(-40) in all), summed from the top in value order: the
 //           value v* at which the running mass reaches top_p * S and the
-//           number j of its occurrences kept, equal values keeping the
-//           lower ids first (sampler.py:81-89, stable order of equal
-//           probabilities)
+//           number j of its occurrences kept (sampler.py:81-89), spread
+//           over their ids (spread_kept, cx_device.hpp)
 //   top-k   the k-th largest element's value from the counts, every value
 //           at or above it kept (sampler.py:76-79, ties included); top-p
 //           cuts that set unrenormalised, so where its mass falls short of
@@ -22,9 +21,9 @@
 //   min-p   kept values are those whose term reaches min_p times the top
 //           term, 1 (sampler.py:91-93)
 //   ranges  per range, the kept mass above v* and the number of v*'s
-//           occurrences, which hands the j kept occurrences of v* to the
-//           ranges in id order: from the copies when every kept value lies
-//           in the copied window, else by a second pass over the row
+//           occurrences, whose running count gives each range's share of
+//           the j kept occurrences: from the copies when every kept value
+//           lies in the copied window, else by a second pass over the row
 //   draw    the range holding u * Z (Z the kept total), then its sixteenth
 //           (each wave sums one), then one wave's scan of that sixteenth in
 //           id order (sampler.py:126-127: choice == searchsorted(cumsum, u,
@@ -218,7 +217,7 @@ __device__ inline bool deep16_row_impl(const SampleArgs& A, int row, const cx_ro
       topk_all = !(P.top_p < 1.0) || sh.kqd[2] < P.top_p * S - DTOL * S;
     }
   }
-  // kept: key > kc, or key == kc among its first jk occurrences in id order
+  // kept: key > kc, or key == kc among the jk of its cntc occurrences that survive
   uint32_t kc = kspan - 1;
   int jk = 0;
   double termc = 0.0;
@@ -359,32 +358,34 @@ __device__ inline bool deep16_row_impl(const SampleArgs& A, int row, const cx_ro
     }
   }
   __syncthreads();
+  // v*'s kept occurrences in the id ranges: of its cntc occurrences jk are
+  // kept, spread over their ids -- the first R hold spread_kept(R) of them
+  auto kept_between = [&](int r0, int r1) -> int {
+    return (int)(spread_kept(r1, jk, cntc) - spread_kept(r0, jk, cntc));
+  };
   double Z = 0.0;
   {
-    int rem = jk, call = 0;
+    int call = 0;
     for (int k = 0; k < NWAVE; ++k) {
-      const int keep = min(sh.we[k], rem);
-      rem -= keep;
+      Z += sh.wm[k] + (double)kept_between(call, call + sh.we[k]) * termc;
       call += sh.we[k];
-      Z += sh.wm[k] + (double)keep * termc;
     }
     if (call != cntc) return false;                  // (cannot happen: the passes agree)
   }
   if (!(Z > 0.0)) return false;
   const double tolZ = DTOL * Z;
   const double t2 = A.u[row] * Z;
-  // the range holding t2, and how many of its occurrences of v* are kept
-  int wr = -1, keepr = 0;
+  // the range holding t2, and the occurrences of v* before it
+  int wr = -1, baser = 0;
   double off = 0.0;
   {
     double o = 0.0;
-    int rem = jk;
+    int before = 0;
     for (int k = 0; k < NWAVE && wr < 0; ++k) {
-      const int keep = min(sh.we[k], rem);
-      rem -= keep;
-      const double m = sh.wm[k] + (double)keep * termc;
-      if (o + m > t2) { wr = k; off = o; keepr = keep; }
+      const double m = sh.wm[k] + (double)kept_between(before, before + sh.we[k]) * termc;
+      if (o + m > t2) { wr = k; off = o; baser = before; }
       o += m;
+      before += sh.we[k];
     }
   }
   __syncthreads();
@@ -412,16 +413,15 @@ __device__ inline bool deep16_row_impl(const SampleArgs& A, int row, const cx_ro
     if (l == 0) { sh.wm[w] = m; sh.we[w] = c; }
   }
   __syncthreads();
-  int sr = -1, keeps = 0;
+  int sr = -1, bases = 0;
   {
     double o = off;
-    int rem = keepr;
+    int before = baser;
     for (int k = 0; k < NWAVE && sr < 0; ++k) {
-      const int keep = min(sh.we[k], rem);
-      rem -= keep;
-      const double m = sh.wm[k] + (double)keep * termc;
-      if (o + m > t2) { sr = k; off = o; keeps = keep; }
+      const double m = sh.wm[k] + (double)kept_between(before, before + sh.we[k]) * termc;
+      if (o + m > t2) { sr = k; off = o; bases = before; }
       o += m;
+      before += sh.we[k];
     }
   }
   // ---- one wave scans the sixteenth in id order: the first element whose
@@ -445,7 +445,8 @@ __device__ inline bool deep16_row_impl(const SampleArgs& A, int row, const cx_ro
           const int y = __shfl_up(ie, o);
           if (l >= o) ie += y;
         }
-        int rank = eqw + ie - ne;                    // occurrences of v* before this lane's
+        // occurrences of v* before this lane's, as the spread remainder
+        int rem = spread_rem(bases + eqw + ie - ne, jk, cntc);
         double q[16];
         double ls = 0.0;
 #pragma unroll
@@ -455,7 +456,7 @@ __device__ inline bool deep16_row_impl(const SampleArgs& A, int row, const cx_ro
             const uint32_t code = deep_code(wd, j);
             const uint32_t key = d16_key(code);
             if (key > kc) v = kept_term(key, code);
-            else if (key == kc) { v = rank < keeps ? termc : 0.0; ++rank; }
+            else if (key == kc) v = spread_step(rem, jk, cntc) ? termc : 0.0;
           }
           q[j] = v;
           ls += v;

@@ -247,9 +247,49 @@ __device__ __forceinline__ void block_argmax(double& v, int& i, double* sv, int*
   __syncthreads();
 }
 
+// ------------------------------------------------------------ tie groups
+// A prefix cut in (key desc, id asc) order that ends inside a group of equal
+// keys keeps j of the group's n members (numpy's argsort, sampler.py:82,103,
+// leaves which ones unspecified).  The survivors are spread evenly over the
+// group's ids: of its first R members (ascending id), spread_kept(R, j, n) =
+// floor((2 R j + n - 1) / (2 n)) survive, so member r survives iff
+// spread_kept(r + 1) > spread_kept(r), and the members of an id range
+// [R0, R1) hold spread_kept(R1) - spread_kept(R0) survivors.  (Lower ids
+// first would keep the group's lowest ids: a systematic bias of the draw
+// towards low ids that numpy's unstable orders do not have.)
+// (Group sizes are below 2^21, so x = 2 R j + n - 1 < 2^43 is exact in fp64,
+// and so is floor(x / 2n) of the correctly rounded quotient: a quotient below
+// an integer lies at least 1 / 2n below it, far more than its rounding error
+// for x < 2^53.  A 64-bit integer division would expand into a long, register
+// hungry sequence at every use.)
+__device__ __forceinline__ long long spread_kept(long long R, long long j, long long n) {
+  if (j <= 0 || n <= 0) return 0;
+  if (j >= n) return R;
+  const double x = (double)(2 * R * j + n - 1);
+  return (long long)floor(x / (double)(2 * n));
+}
+__device__ __forceinline__ bool spread_keeps(long long r, long long j, long long n) {
+  return spread_kept(r + 1, j, n) > spread_kept(r, j, n);
+}
+// The same decision for consecutive members without a division each: with
+// x_r = 2 r j + n - 1, member r survives iff (x_r mod 2n) + 2j >= 2n, and
+// x_{r+1} mod 2n follows by one addition.  spread_rem gives x_r mod 2n (n >
+// 0); spread_step decides member r from it and advances it to r + 1.
+__device__ __forceinline__ int spread_rem(long long r, long long j, long long n) {
+  if (n <= 0) return 0;
+  const double x = (double)(2 * r * j + n - 1), d = (double)(2 * n);
+  return (int)(x - floor(x / d) * d);
+}
+__device__ __forceinline__ bool spread_step(int& rem, int j, int n) {
+  const bool keep = rem + 2 * j >= 2 * n;
+  rem += 2 * j;
+  rem -= rem >= 2 * n ? 2 * n : 0;
+  return keep;
+}
+
 // ------------------------------------------------------------ sort records
-// A record orders by key descending, then by idx ascending (NumPy's stable
-// tie rule: equal probabilities keep the lower token id first).
+// A record orders by key descending, then by idx ascending (a total order:
+// tie groups are contiguous and sorted by id, as the tie rule above needs).
 struct Rec {
   uint64_t key;
   int32_t idx;
@@ -344,7 +384,7 @@ __device__ __forceinline__ void own_stage(Rec (&r)[R], const bool (&have)[R], in
 // thread's own elements, strides from 64 to WG / 2 exchange through LDS,
 // smaller strides through cross-lane shuffles.
 template <int R = 2>
-__device__ inline void block_sort(uint64_t* k, int32_t* i, int32_t* a, int n) {
+__device__ __forceinline__ void block_sort(uint64_t* k, int32_t* i, int32_t* a, int n) {
   static_assert(R == 2 || R == 4, "R");
   int np = 2;
   while (np < n) np <<= 1;
@@ -417,7 +457,7 @@ __device__ inline void block_sort(uint64_t* k, int32_t* i, int32_t* a, int n) {
 // Inclusive prefix sum of v[0..n), n <= R * WG, in place (fp64).  Thread t
 // owns elements R t .. R t + R - 1.
 template <int R = 2>
-__device__ inline void block_scan(double* v, int n, double* scratch) {
+__device__ __forceinline__ void block_scan(double* v, int n, double* scratch) {
   static_assert(R == 2 || R == 4, "R");
   const int t = threadIdx.x;
   double x[R];

@@ -6,7 +6,9 @@
 // the reference's filters on fp64 probabilities, with bucketed cuts (a
 // sort of the whole region only when a cut's bucket overflows):
 //   top-k   sampler.py:76-79  keep every value >= the k-th largest
-//   top-p   sampler.py:81-89  shortest prefix (value desc, id asc) with cum >= p
+//   top-p   sampler.py:81-89  shortest prefix (value desc, id asc) with cum >= p;
+//                             the cut value's group keeps its survivors spread
+//                             over its ids (spread_kept, cx_device.hpp)
 //   min-p   sampler.py:91-93  keep P >= min_p * max P
 // then normalises (:123-126) and draws by inverse CDF in token-id order
 // (:127, Generator.choice == searchsorted(cumsum/last, u, 'right')).
@@ -111,6 +113,7 @@ struct PrefixCut {
   double total;     // weight of all eligible entries
   uint64_t key;     // the cut entry's order key and token id
   int32_t idx;
+  int g0, g1;       // the cut key's entries: positions [g0, g1) of the sorted bucket
 };
 
 // The first eligible entry, in the order (bucket_of ascending, then key
@@ -188,9 +191,14 @@ __device__ inline void prefix_cut(int E, const int32_t* sidx, BucketOf bucket_of
     const double cum = based + incl, prv = based + (incl - w);
     const uint64_t hb = ballot(l < n && (strict ? cum > tgt : cum >= tgt));
     const int pos = hb ? __builtin_ctzll(hb) : n - 1;
+    // equal keys land in one bucket: the cut key's whole group is here,
+    // contiguous and in ascending ids
+    const uint64_t gb = ballot(l < n && r[0].key == lane_read(r[0].key, pos));
     if (l == pos) {
       out.found = 1; out.overflow = 0; out.bucket = bc; out.pos = pos; out.n = n;
       out.cum = cum; out.prev = prv; out.total = total; out.key = r[0].key; out.idx = r[0].idx;
+      out.g0 = __builtin_ctzll(gb);
+      out.g1 = 64 - __builtin_clzll(gb);
     }
   }
   __syncthreads();
@@ -265,7 +273,8 @@ __device__ inline int finish_bucketed(const SampleArgs& A, int row, const cx_row
     }
   }
   // ---- top-p on the unrenormalised vector: the shortest prefix in (value
-  // desc, id asc) order whose running mass reaches top_p
+  // desc, id asc) order whose running mass reaches top_p; of the cut
+  // value's group, the survivors spread over its ids
   if (P.top_p < 1.0) {
     prefix_cut(E, sidx, vbucket, vkey, mass, kept, FX_MASS, P.top_p, false, false, bm, gk, gi, ga,
                red_d, red_i, pc);
@@ -274,11 +283,12 @@ __device__ inline int finish_bucketed(const SampleArgs& A, int row, const cx_row
     if (pc.found) {
       const double cm = pc.cum, cp = pc.prev;
       near = fabs(cm - P.top_p) <= tol * cm || (cp > 0.0 && fabs(cp - P.top_p) <= tol * cp);
-      const int bc = pc.bucket, pos = pc.pos;
+      const int bc = pc.bucket, pos = pc.pos, g0 = pc.g0, g1 = pc.g1;
       for (int j = t; j < E; j += WG)
         if (kf[j] && vbucket(j) >= bc) kf[j] = 0;
       __syncthreads();
-      if (t <= pos) kf[ga[t]] = 1;       // the cut bucket's entries up to the cut
+      // the cut bucket's entries before the cut value, and its group's survivors
+      if (t < g0 || (t < g1 && spread_keeps(t - g0, pos + 1 - g0, g1 - g0))) kf[ga[t]] = 1;
       __syncthreads();
       complete = true;
     } else {
@@ -333,6 +343,7 @@ __device__ inline int finish_row_fast(const SampleArgs& A, int row, const cx_row
   constexpr int R = CAP / WG;
   __shared__ int f_n;
   __shared__ int f_j;
+  __shared__ int f_g[2];
   const int t = threadIdx.x;
   const int nsp = A.nsplit;
   const SplitStats* st = A.stats + (size_t)row * nsp;
@@ -497,6 +508,37 @@ __device__ inline int finish_row_fast(const SampleArgs& A, int row, const cx_row
     if (m < nk) {
       near = fabs(sc[m] - P.top_p) <= tol * sc[m] ||
              (m > 0 && fabs(sc[m - 1] - P.top_p) <= tol * sc[m - 1]);
+      // the cut value's group, positions [g0, g1) (ascending ids), keeps
+      // m + 1 - g0 members spread over its ids: move them to [g0, m] so the
+      // kept entries stay a prefix (the group's probabilities are equal)
+      if (t == 0) { f_g[0] = m; f_g[1] = m + 1; }
+      __syncthreads();
+      for (int j = t; j < nk; j += WG)
+        if (skey[j] == skey[m]) { atomicMin(&f_g[0], j); atomicMax(&f_g[1], j + 1); }
+      __syncthreads();
+      const int g0 = f_g[0], g1 = f_g[1];
+      if (g1 > m + 1) {
+        const int jg = m + 1 - g0, ng = g1 - g0;
+        uint64_t mk[R];
+        int32_t mi[R];
+#pragma unroll
+        for (int q = 0; q < R; ++q) {
+          const int j = g0 + q * WG + t;
+          mk[q] = j < g1 ? skey[j] : 0ull;
+          mi[q] = j < g1 ? sidx[j] : 0;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < R; ++q) {
+          const int r = q * WG + t;
+          if (r < ng && spread_keeps(r, jg, ng)) {
+            const int d = g0 + (int)spread_kept(r, jg, ng);
+            skey[d] = mk[q];
+            sidx[d] = mi[q];
+          }
+        }
+        __syncthreads();
+      }
       nk = m + 1;
       complete = true;
     } else {

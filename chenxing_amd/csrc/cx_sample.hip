@@ -808,6 +808,7 @@ __device__ inline int lean_decide(const cx_row_params& P, const CX_LDS uint64_t*
   }
   // (2) probabilities of the kept prefix; top-p on the unrenormalised vector
   const double Pj = l < n ? exp2(key2d(key) * kc - Rb) / S : 0.0;
+  bool keep = l < n;
   if (P.top_p < 1.0) {                                 // sampler.py:81-89
     const double cum = wave_scan_dpp(Pj);
     const uint64_t b = ballot(l < n && cum >= P.top_p);
@@ -817,7 +818,13 @@ __device__ inline int lean_decide(const cx_row_params& P, const CX_LDS uint64_t*
       const double cm = lane_read(cum, mm);
       const double cp = lane_read(cum, mm > 0 ? mm - 1 : 0);
       near = fabs(cm - P.top_p) <= tol * cm || (mm > 0 && fabs(cp - P.top_p) <= tol * cp);
-      n = mm + 1;
+      // the group of the cut entry's value (contiguous lanes, ascending ids,
+      // all inside the top-k set) keeps mm + 1 - g0 of its members, spread
+      // over its ids
+      const uint64_t kcut = lane_read(key, mm);
+      const uint64_t g = ballot(l < n && key == kcut);
+      const int g0 = __builtin_ctzll(g), g1 = 64 - __builtin_clzll(g);
+      keep = l < g0 || (l < g1 && spread_keeps(l - g0, mm + 1 - g0, g1 - g0));
     } else {
       const double cl = lane_read(cum, n - 1);
       near = fabs(cl - P.top_p) <= tol * cl;
@@ -826,16 +833,15 @@ __device__ inline int lean_decide(const cx_row_params& P, const CX_LDS uint64_t*
   }
   if (P.min_p > 0.0) {                                 // sampler.py:91-93
     const double floor_p = P.min_p * lane_read(Pj, 0);
-    const uint64_t b = ballot(l < n && Pj < floor_p);
-    if (b) n = __builtin_ctzll(b);
+    keep = keep && !(Pj < floor_p);
   }
   // (3) normalise and draw in token-id order (sampler.py:123-127; choice ==
   // searchsorted(cumsum / last, u, 'right')): the kept mass goes to its id
   // rank, lane l sums id ranks 4l .. 4l + 3, and a scan over the lanes gives
   // the cumulative mass at every id rank
-  const double qv = l < n ? Pj : 0.0;
+  const double qv = keep ? Pj : 0.0;
   const double Z = wave_reduce(qv, OpAdd());
-  if (l < n) L->oq[rid] = qv / Z;
+  if (keep) L->oq[rid] = qv / Z;
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   __builtin_amdgcn_wave_barrier();
   static_assert(LEAN_CAP == 4 * 64, "four id ranks per lane");
@@ -856,7 +862,7 @@ __device__ inline int lean_decide(const cx_row_params& P, const CX_LDS uint64_t*
   for (int i = 3; i >= 0; --i)
     if (4 * l + i < nlist && (base + f[i]) / last > u) first = 4 * l + i;
   const uint64_t b = ballot(first != INT_MAX);
-  tok = b ? L->oid[lane_read(first, __builtin_ctzll(b))] : wave_reduce(l < n ? idx : -1, OpMax());
+  tok = b ? L->oid[lane_read(first, __builtin_ctzll(b))] : wave_reduce(keep ? idx : -1, OpMax());
   return LEAN_DONE;
 }
 

@@ -11,9 +11,13 @@
 //   pass B   S = sum exp((x - M) / T)  (and the T = 1 sum for the underflow test)
 //   select   top-k threshold (count select) and the top-p and typical-p cuts
 //            (mass select): histogram passes over an exactly narrowing key
-//            range, then the last bucket is gathered into LDS and sorted
-//   draw     per-thread sums over contiguous id ranges, block scan, and a
-//            sequential scan inside the range that holds u (token-id order)
+//            range, then the last bucket is gathered into LDS and sorted; a
+//            cut inside a group of equal keys keeps j of its n members,
+//            spread over their ids (spread_kept, cx_device.hpp)
+//   draw     per-wave sums over contiguous id ranges, and a scan in id order
+//            of the range that holds u (the passes after a cut visit the row
+//            in these wave ranges, so a group member's rank is a running
+//            count)
 //
 // slow_kernel (cx_slow.hip) runs it for the rows the fused path left
 // pending.  Rows are re-read from memory for every pass; such rows are rare
@@ -114,32 +118,42 @@ __device__ __forceinline__ double mass_of(const SlowRow& R, double v) {
   return R.direct ? v : exp((v - R.M) * R.invT) / R.S;
 }
 
-// Boundary of a prefix in (key desc, idx asc) order: element e is inside iff
-// key > k || (key == k && idx <= i).
+// Boundary of a prefix in (key desc, idx asc) order over the eligible
+// elements: keys above k are inside, keys below outside; of the n eligible
+// elements whose key equals k, j are inside, spread over their ids -- the
+// one of rank r (members with a lower id before it) is inside iff
+// spread_keeps(r, j, n) (cx_device.hpp).  j >= n: the whole group is inside
+// (top-k keeps its ties, and a cut that ends a group splits nothing).
 struct Cut {
   uint64_t k;
-  int i;
+  int n, j;
 };
-__device__ __forceinline__ bool inside(const Cut& c, uint64_t key, int idx) {
-  return key > c.k || (key == c.k && idx <= c.i);
+__device__ __forceinline__ Cut cut_at(uint64_t k) {
+  Cut c;
+  c.k = k;
+  c.n = 0;
+  c.j = 0;
+  return c;
+}
+__device__ __forceinline__ bool cut_split(const Cut& c) { return c.j < c.n; }
+__device__ __forceinline__ bool inside(const Cut& c, uint64_t key, int rank) {
+  return key > c.k || (key == c.k && (c.j >= c.n || spread_keeps(rank, c.j, c.n)));
 }
 
 struct Filters {
-  Cut rank;          // top-k / top-p prefix
+  Cut rank;          // top-k / top-p prefix (value order)
   double floor_p;    // min-p floor on P (0 = off)
   bool typ;          // typical-p cut active
   double H;          // entropy for the typical order
-  Cut tcut;          // typical prefix in (-shift desc, idx asc) order
+  Cut tcut;          // typical prefix in (-|log P + H| desc, idx asc) order
+  bool want_tk;      // the visits compute the typical order key
+  int* b1;           // [NWAVE] rank's group members before each wave range
+  int* b2;           // [NWAVE] tcut's group members before each wave range
 };
 
 __device__ __forceinline__ uint64_t typ_key(double P, double H) {
   double lp = log(P > 1e-38 ? P : 1e-38);
   return d2key(-fabs(lp + H));
-}
-
-// Kept by top-k, top-p and min-p (the typical cut is applied separately).
-__device__ __forceinline__ bool kept_rank(const Filters& F, uint64_t key, int idx, double P) {
-  return inside(F.rank, key, idx) && P >= F.floor_p;
 }
 
 struct SlowLds {
@@ -151,35 +165,110 @@ struct SlowLds {
   double* gm;        // [SCAP]
 };
 
-// Order key of element (v, idx) for a selection: rank order (value) or the
-// typical order (-|log P + H|).  Returns false if the element is not eligible.
-template <bool TYP>
-__device__ __forceinline__ bool sel_key(const SlowRow& R, const Filters& F, int i, double v,
-                                        uint64_t& key, double& m) {
-  uint64_t vk = d2key(v);
-  if (!TYP) {
-    key = vk;
-    m = 0.0;
-    return true;
+// ---- wave-range traversal
+// Once a cut splits a tie group, whether a member is kept depends on how
+// many members precede it in id order.  The passes after the cuts therefore
+// visit the row in wave ranges: wave w takes ids [w WL, (w + 1) WL) (WL a
+// multiple of 64), 64 consecutive ids at a time, lane l id base + l, so a
+// member's rank is its wave's base count (Filters::b1, b2) plus a ballot
+// prefix.  Control flow is wave-uniform; fn may use wave operations.
+__device__ __forceinline__ int wave_span(int V) {
+  return ((V + NWAVE * 64 - 1) / (NWAVE * 64)) * 64;
+}
+
+// One element as the filters see it.
+struct SElem {
+  int i;             // token id
+  bool valid;        // i < the range's end
+  double v;          // penalised fp64 value (the mass itself for direct rows)
+  uint64_t key;      // d2key(v)
+  double P;          // post-temperature probability
+  bool kr;           // kept by top-k, top-p and min-p
+  uint64_t tk;       // typical order key (F.want_tk, else 0)
+  bool kt;           // kept by every filter
+};
+
+// Visits ids [lo, hi) by the calling wave, with r1 / r2 members of the rank
+// and typical groups before lo.
+template <typename Fn>
+__device__ __forceinline__ void visit_range(const SlowRow& R, const Filters& F, int lo, int hi,
+                                            int r1, int r2, Fn fn) {
+  const int l = lane_id();
+  const bool s1 = cut_split(F.rank);
+  const bool s2 = F.want_tk && F.typ && cut_split(F.tcut);
+  for (int base = lo; base < hi; base += 64) {
+    SElem e;
+    e.i = base + l;
+    e.valid = e.i < hi;
+    e.v = e.valid ? value_at(R, e.i) : 0.0;
+    e.key = d2key(e.v);
+    e.P = mass_of(R, e.v);
+    const uint64_t m1 = ballot(s1 && e.valid && e.key == F.rank.k);
+    const int rk1 = r1 + lanes_below(m1);
+    r1 += __popcll(m1);
+    e.kr = e.valid && inside(F.rank, e.key, rk1) && e.P >= F.floor_p;
+    e.tk = 0ull;
+    e.kt = e.kr;
+    if (F.want_tk) {
+      e.tk = typ_key(e.P, F.H);
+      const uint64_t m2 = ballot(s2 && e.kr && e.tk == F.tcut.k);
+      const int rk2 = r2 + lanes_below(m2);
+      r2 += __popcll(m2);
+      if (F.typ) e.kt = e.kr && inside(F.tcut, e.tk, rk2);
+    }
+    fn(e);
   }
-  double P = mass_of(R, v);
-  if (!kept_rank(F, vk, i, P)) return false;
-  key = typ_key(P, F.H);
-  m = P;
-  return true;
+}
+// The whole row, each wave its range.
+template <typename Fn>
+__device__ __forceinline__ void visit_row(const SlowRow& R, const Filters& F, Fn fn) {
+  const int WL = wave_span(R.V), w = wave_id();
+  const int lo = min(R.V, w * WL), hi = min(R.V, lo + WL);
+  visit_range(R, F, lo, hi, F.b1[w], F.b2[w], fn);
+}
+
+// Each wave's count of the elements fn(e) selects, and their exclusive scan
+// over the waves into b[NWAVE] (all threads; ends with a barrier).
+template <typename Sel>
+__device__ __forceinline__ void group_bases(const SlowRow& R, const Filters& F, int* b, Sel sel) {
+  int c = 0;
+  visit_row(R, F, [&](const SElem& e) { c += __popcll(ballot(e.valid && sel(e))); });
+  __shared__ int gb_cnt[NWAVE];
+  if (lane_id() == 0) gb_cnt[wave_id()] = c;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int run = 0;
+    for (int w = 0; w < NWAVE; ++w) { b[w] = run; run += gb_cnt[w]; }
+  }
+  __syncthreads();
 }
 
 // Select the shortest prefix, in (key desc, idx asc) order over the eligible
-// elements, that holds `target` elements (COUNT) or `target` mass (MASS).
-// Returns false if the eligible total never reaches the target.
+// elements, that holds `target` elements (COUNT) or `target` mass (MASS):
+// the cut key, its group's eligible members n and how many of them the
+// prefix takes, j.  Eligible: inside `elig` (a cut that splits no group),
+// keyed by value; or with TYP, kept by the rank filters of F, keyed by the
+// typical order key.  Returns false if the eligible total never reaches the
+// target.
 template <bool TYP, bool MASS>
-__device__ bool select_prefix(const SlowRow& R, const Filters& F, const Cut& elig, double target,
+__device__ __forceinline__ bool select_prefix(const SlowRow& R, const Filters& F, const Cut& elig, double target,
                               uint64_t klo, uint64_t khi, SlowLds& L, Cut& out, double* red_d,
                               int* red_i) {
   __shared__ uint64_t sh_u[4];
   __shared__ double sh_d[2];
-  __shared__ int sh_i[2];
+  __shared__ int sh_i[3];
   const int t = threadIdx.x;
+  // the element's order key and weight, if eligible
+  auto pick = [&](const SElem& e, uint64_t& key, double& m) -> bool {
+    if (TYP) {
+      key = e.tk;
+      m = e.P;
+      return e.kr;
+    }
+    key = e.key;
+    m = MASS ? e.P : 1.0;
+    return e.valid && inside(elig, e.key, 0);
+  };
   double above = 0.0;                           // count or mass of elements with key > khi
   for (int level = 0; level < 8; ++level) {
     uint64_t D = khi - klo;
@@ -187,17 +276,15 @@ __device__ bool select_prefix(const SlowRow& R, const Filters& F, const Cut& eli
     while ((D >> sh) >= (uint64_t)NB) ++sh;
     for (int b = t; b < NB; b += WG) { L.cnt[b] = 0u; L.mass[b] = 0.0; }
     __syncthreads();
-    for (int i = t; i < R.V; i += WG) {
-      double v = value_at(R, i);
+    visit_row(R, F, [&](const SElem& e) {
       uint64_t key;
       double m;
-      if (!sel_key<TYP>(R, F, i, v, key, m)) continue;
-      if (!TYP && !inside(elig, key, i)) continue;
-      if (key < klo || key > khi) continue;
-      int b = (int)((key - klo) >> sh);
-      atomicAdd(&L.cnt[b], 1u);
-      if (MASS) atomicAdd(&L.mass[b], TYP ? m : mass_of(R, v));
-    }
+      if (pick(e, key, m) && key >= klo && key <= khi) {
+        int b = (int)((key - klo) >> sh);
+        atomicAdd(&L.cnt[b], 1u);
+        if (MASS) atomicAdd(&L.mass[b], m);
+      }
+    });
     __syncthreads();
     if (t == 0) {
       int b = NB - 1;
@@ -225,77 +312,40 @@ __device__ bool select_prefix(const SlowRow& R, const Filters& F, const Cut& eli
     klo = nlo;
     khi = nhi;
     __syncthreads();
-    if (nb <= SCAP || klo == khi) {
-      // gather the bucket (for a single-key bucket larger than SCAP only the
-      // lowest ids are needed: the cut falls at a count known from its mass)
-      if (nb > SCAP) {
-        // all share one key (and one mass): how many of them complete the prefix
-        double unit = 0.0;
-        if (t == 0) {
-          unit = MASS ? (L.mass[bstar] / (double)nb) : 1.0;
-          double need = (target - above) / unit;
-          long c = (long)ceil(need);
-          if (c < 1) c = 1;
-          if (c > nb) c = nb;
-          sh_i[0] = (int)c;
-        }
-        __syncthreads();
-        const int c = sh_i[0];
-        // the c-th smallest id among the bucket: count select over ids
-        int lo_id = 0, hi_id = R.V - 1, before = 0;
-        for (int lev = 0; lev < 4; ++lev) {
-          int span = hi_id - lo_id + 1;
-          int ish = 0;
-          while ((span >> ish) >= NB) ++ish;
-          for (int b = t; b < NB; b += WG) L.cnt[b] = 0u;
-          __syncthreads();
-          for (int i = lo_id + t; i <= hi_id; i += WG) {
-            double v = value_at(R, i);
-            uint64_t key;
-            double m;
-            if (!sel_key<TYP>(R, F, i, v, key, m)) continue;
-            if (!TYP && !inside(elig, key, i)) continue;
-            if (key != klo) continue;
-            atomicAdd(&L.cnt[(i - lo_id) >> ish], 1u);
-          }
-          __syncthreads();
-          if (t == 0) {
-            int b = 0, run = before;
-            for (; b < NB - 1; ++b) {
-              if (run + (int)L.cnt[b] >= c) break;
-              run += (int)L.cnt[b];
-            }
-            sh_i[0] = b;
-            sh_i[1] = run;
-          }
-          __syncthreads();
-          before = sh_i[1];
-          lo_id = lo_id + (sh_i[0] << ish);
-          hi_id = min(hi_id, lo_id + (1 << ish) - 1);
-          __syncthreads();
-          if (ish == 0) break;
-        }
-        out.k = klo;
-        out.i = lo_id;
-        return true;
+    if (nb > SCAP && klo == khi) {
+      // one key (and one weight) for the whole bucket: the prefix takes c of
+      // its nb members, a count known from the weight
+      if (t == 0) {
+        const double unit = MASS ? (L.mass[bstar] / (double)nb) : 1.0;
+        long c = (long)ceil((target - above) / unit);
+        if (c < 1) c = 1;
+        if (c > nb) c = nb;
+        sh_i[2] = (int)c;
       }
+      __syncthreads();
+      out.k = klo;
+      out.n = nb;
+      out.j = sh_i[2];
+      __syncthreads();
+      return true;
+    }
+    if (nb <= SCAP) {
+      // gather the bucket: the cut key's whole group is in it
       __shared__ int gn;
       if (t == 0) gn = 0;
       __syncthreads();
-      for (int i = t; i < R.V; i += WG) {
-        double v = value_at(R, i);
+      visit_row(R, F, [&](const SElem& e) {
         uint64_t key;
         double m;
-        if (!sel_key<TYP>(R, F, i, v, key, m)) continue;
-        if (!TYP && !inside(elig, key, i)) continue;
-        if (key < klo || key > khi) continue;
-        int pos = atomicAdd(&gn, 1);
-        if (pos < SCAP) {
-          L.gk[pos] = key;
-          L.gi[pos] = i;
-          L.gm[pos] = MASS ? (TYP ? m : mass_of(R, v)) : 1.0;
+        if (pick(e, key, m) && key >= klo && key <= khi) {
+          int pos = atomicAdd(&gn, 1);
+          if (pos < SCAP) {
+            L.gk[pos] = key;
+            L.gi[pos] = e.i;
+            L.gm[pos] = m;
+          }
         }
-      }
+      });
       __syncthreads();
       const int n = min(gn, SCAP);   // >= 1: the bucket was counted non-empty
       for (int j = t; j < n; j += WG) L.ga[j] = j;
@@ -308,19 +358,24 @@ __device__ bool select_prefix(const SlowRow& R, const Filters& F, const Cut& eli
           run += L.gm[L.ga[j]];
           if (run >= target) break;
         }
+        // the cut key's group: sorted positions [g0, g1)
+        int g0 = j, g1 = j + 1;
+        while (g0 > 0 && L.gk[g0 - 1] == L.gk[j]) --g0;
+        while (g1 < n && L.gk[g1] == L.gk[j]) ++g1;
         sh_u[0] = L.gk[j];
-        sh_i[0] = L.gi[j];
+        sh_i[0] = g1 - g0;
+        sh_i[1] = j + 1 - g0;
       }
       __syncthreads();
       out.k = sh_u[0];
-      out.i = sh_i[0];
+      out.n = sh_i[0];
+      out.j = sh_i[1];
       __syncthreads();
       return true;
     }
   }
   // unreachable for 64-bit keys (each level narrows the range by NB)
-  out.k = klo;
-  out.i = INT_MAX;
+  out = cut_at(klo);
   return true;
 }
 
@@ -332,7 +387,8 @@ __device__ __forceinline__ int lin_bucket(double v, double lo, double inv) {
 }
 
 // Top-p over a logit row with no top-k before it (sampler.py:81-89): the
-// shortest prefix in (value desc, idx asc) order holding `target` mass.
+// shortest prefix in (value desc, idx asc) order holding `target` mass, as a
+// Cut (the cut value's group and how many of it the prefix takes).
 // Level 0 splits the values in [vlo, M] linearly into NB buckets (values far
 // apart land in different buckets, so the mass atomics rarely collide); a
 // level keeps the bucket the cut falls in and splits it again, and a bucket
@@ -342,7 +398,7 @@ __device__ __forceinline__ int lin_bucket(double v, double lo, double inv) {
 // this cannot decide -- the elements at or above vlo hold less than the
 // target, or MAXLV levels leave a bucket larger than SCAP -- and the
 // caller then runs select_prefix.  tsum: WG doubles of LDS.
-__device__ bool select_mass_linear(const SlowRow& R, double target, double vlo, SlowLds& L,
+__device__ __forceinline__ bool select_mass_linear(const SlowRow& R, double target, double vlo, SlowLds& L,
                                    double* tsum, Cut& out, double* red_d, int* red_i) {
   static_assert(NB == WG, "one bucket per thread");
   constexpr int MAXLV = 4;
@@ -411,8 +467,15 @@ __device__ bool select_mass_linear(const SlowRow& R, double target, double vlo, 
       block_scan(tsum, NB, red_d);
       const int hit = (t < n && (above_b + tsum[t] >= target || t == n - 1)) ? t : INT_MAX;
       const int j = block_min(hit, red_i, INT_MAX);
-      out.k = L.gk[j];
-      out.i = L.gi[j];
+      // the cut value's group (equal values share every level's bucket):
+      // sorted positions [g0, g1)
+      const uint64_t kj = L.gk[j];
+      const bool ing = t < n && L.gk[t] == kj;
+      const int g0 = block_min(ing ? t : INT_MAX, red_i, INT_MAX);
+      const int g1 = block_max(ing ? t + 1 : 0, red_i, 0);
+      out.k = kj;
+      out.n = g1 - g0;
+      out.j = j + 1 - g0;
       __syncthreads();
       return true;
     }
@@ -579,21 +642,24 @@ __device__ inline void slow_row(const SampleArgs& A, int row, unsigned char* dyn
   }
 
   // ---- rank-order filters
+  __shared__ int s_b1[NWAVE], s_b2[NWAVE];
+  if (t < NWAVE) { s_b1[t] = 0; s_b2[t] = 0; }
   Filters F;
-  F.rank.k = 0;
-  F.rank.i = INT_MAX;
+  F.rank = cut_at(0ull);
   F.floor_p = 0.0;
   F.typ = false;
   F.H = 0.0;
+  F.tcut = cut_at(0ull);
+  F.want_tk = false;
+  F.b1 = s_b1;
+  F.b2 = s_b2;
+  __syncthreads();
   const uint64_t kmax = d2key(mx), kmin = d2key(mn);
-  Cut all;
-  all.k = 0;
-  all.i = INT_MAX;
+  const Cut all = cut_at(0ull);
   if (P.top_k > 0 && P.top_k < V) {                          // sampler.py:76-79
     Cut c;
     select_prefix<false, false>(R, F, all, (double)P.top_k, kmin, kmax, L, c, red_d, red_i);
-    F.rank.k = c.k;                                          // ties at the k-th value stay
-    F.rank.i = INT_MAX;
+    F.rank = cut_at(c.k);                                    // ties at the k-th value stay
   }
   if (P.top_p < 1.0) {                                       // sampler.py:81-89
     Cut c;
@@ -611,48 +677,52 @@ __device__ inline void slow_row(const SampleArgs& A, int row, unsigned char* dyn
       if (select_prefix<false, true>(R, F, F.rank, P.top_p, lo, kmax, L, c, red_d, red_i))
         F.rank = c;
     }
+    // a cut inside a group of equal values: its members' ranks by wave range
+    const uint64_t kc = F.rank.k;
+    if (cut_split(F.rank))
+      group_bases(R, F, s_b1, [&](const SElem& e) { return e.key == kc; });
   }
   if (P.min_p > 0.0) F.floor_p = P.min_p * (1.0 / R.S);      // sampler.py:91-93
   if (P.typical_p < 1.0) {                                   // sampler.py:95-105
     double h = 0.0;
     uint64_t tlo = ~0ull, thi = 0ull;
-    for (int i = t; i < V; i += WG) {
-      double v = value_at(R, i);
-      double p = mass_of(R, v);
-      if (!kept_rank(F, d2key(v), i, p)) continue;
-      h -= p * log(p > 1e-38 ? p : 1e-38);
-    }
+    visit_row(R, F, [&](const SElem& e) {
+      if (e.kr) h -= e.P * log(e.P > 1e-38 ? e.P : 1e-38);
+    });
     F.H = block_sum(h, red_d);
-    for (int i = t; i < V; i += WG) {
-      double v = value_at(R, i);
-      double p = mass_of(R, v);
-      if (!kept_rank(F, d2key(v), i, p)) continue;
-      uint64_t k = typ_key(p, F.H);
-      tlo = k < tlo ? k : tlo;
-      thi = k > thi ? k : thi;
-    }
+    F.want_tk = true;
+    visit_row(R, F, [&](const SElem& e) {
+      if (e.kr) {
+        tlo = e.tk < tlo ? e.tk : tlo;
+        thi = e.tk > thi ? e.tk : thi;
+      }
+    });
     tlo = block_min<unsigned long long>(tlo, (unsigned long long*)red_d, ~0ull);
     thi = block_max<unsigned long long>(thi, (unsigned long long*)red_d, 0ull);
     Cut c;
     F.typ = select_prefix<true, true>(R, F, all, P.typical_p, tlo, thi, L, c, red_d, red_i);
     F.tcut = c;
+    const uint64_t kt = c.k;
+    if (F.typ && cut_split(F.tcut))
+      group_bases(R, F, s_b2, [&](const SElem& e) { return e.kr && e.tk == kt; });
   }
 
-  // ---- normalise and draw in token-id order (sampler.py:123-127)
-  auto kept_mass = [&](int i) -> double {
-    double v = value_at(R, i);
-    double p = mass_of(R, v);
-    uint64_t k = d2key(v);
-    if (!kept_rank(F, k, i, p)) return 0.0;
-    if (F.typ && !inside(F.tcut, typ_key(p, F.H), i)) return 0.0;
-    return p;
-  };
-  const int per = (V + WG - 1) / WG;
-  const int e0 = min(V, t * per), e1 = min(V, e0 + per);
-  double s = 0.0;
-  for (int i = e0; i < e1; ++i) s += kept_mass(i);
-  tsum[t] = s;
-  const double Z = block_sum(s, red_d);
+  // ---- normalise and draw in token-id order (sampler.py:123-127): each
+  // wave's kept mass over its range, the range holding u, then a scan of
+  // that range in id order
+  __shared__ double s_wm[NWAVE];
+  __shared__ int s_found;
+  const int WL = wave_span(V);
+  {
+    double m = 0.0;
+    visit_row(R, F, [&](const SElem& e) { if (e.kt) m += e.P; });
+    m = wave_sum(m);
+    if (lane_id() == 0) s_wm[wave_id()] = m;
+    if (t == 0) s_found = INT_MAX;
+  }
+  __syncthreads();
+  double Z = 0.0;
+  for (int k = 0; k < NWAVE; ++k) Z += s_wm[k];
   if (!(Z > 0.0)) {
     if (A.out_probs) {
       float* pr = A.out_probs + (size_t)row * V;
@@ -665,33 +735,46 @@ __device__ inline void slow_row(const SampleArgs& A, int row, unsigned char* dyn
     return;
   }
   // cdf_i = cumsum(P / Z)_i / cumsum(P / Z)_last; first i with cdf_i > u
-  for (int j = t; j < WG; j += WG) tsum[j] = tsum[j] / Z;
-  __syncthreads();
-  block_scan(tsum, WG, red_d);
-  const double last = tsum[WG - 1];
   const double u = A.u[row];
-  const double prev = t > 0 ? tsum[t - 1] : 0.0;
-  int found = INT_MAX;
-  if (prev / last <= u && tsum[t] / last > u) {
-    double run = prev;
-    for (int i = e0; i < e1; ++i) {
-      double q = kept_mass(i);
-      if (q == 0.0) continue;
-      run += q / Z;
-      if (run / last > u) { found = i; break; }
+  double last = 0.0;
+  for (int k = 0; k < NWAVE; ++k) last += s_wm[k] / Z;
+  {
+    double prev = 0.0;
+    int wr = -1;
+    for (int k = 0; k < NWAVE && wr < 0; ++k) {
+      const double nx = prev + s_wm[k] / Z;
+      if (nx / last > u) wr = k;
+      else prev = nx;
+    }
+    if (wave_id() == wr) {
+      // the group members before this range, and the running sum
+      const int lo = wr * WL, hi = min(V, lo + WL);
+      double run = prev;
+      int found = INT_MAX;
+      visit_range(R, F, lo, hi, F.b1[wr], F.b2[wr], [&](const SElem& e) {
+        if (found != INT_MAX) return;
+        const double q = e.kt ? e.P / Z : 0.0;
+        const double incl = run + wave_scan_dpp(q);
+        const uint64_t hb = ballot(q != 0.0 && incl / last > u);
+        if (hb) found = __builtin_amdgcn_readlane(e.i, __builtin_ctzll(hb));
+        run = __shfl(incl, 63);
+      });
+      if (lane_id() == 0) s_found = found;
     }
   }
-  found = block_min(found, red_i, INT_MAX);
+  __syncthreads();
+  int found = s_found;
   if (found == INT_MAX) {
     // u beyond the last step by rounding: the last kept id
     int lastk = -1;
-    for (int i = t; i < V; i += WG)
-      if (kept_mass(i) > 0.0) lastk = max(lastk, i);
+    visit_row(R, F, [&](const SElem& e) { if (e.kt) lastk = max(lastk, e.i); });
     found = block_max(lastk, red_i, -1);
   }
   if (A.out_probs) {
     float* pr = A.out_probs + (size_t)row * V;
-    for (int i = t; i < V; i += WG) pr[i] = (float)(kept_mass(i) / Z);
+    visit_row(R, F, [&](const SElem& e) {
+      if (e.valid) pr[e.i] = e.kt ? (float)(e.P / Z) : 0.0f;
+    });
   }
   if (t == 0) {
     A.out_id[row] = found;
@@ -728,9 +811,11 @@ __device__ inline void penalties_range(const SampleArgs& A, int row, int i0, int
 //   typical   entropy H over the kept values, then the shortest
 //             prefix in (|log P + H| asc, id asc) order reaching
 //             typical_p                                            :95-105
-// out64[i] = P_i where kept, else 0.  Ties in the two orders go to the lower
-// id (numpy's argsort leaves their order unspecified).  A row holding NaN or
-// a negative value is reported as CX_ROW_ERROR and left unwritten.
+// out64[i] = P_i where kept, else 0.  Of a group of equal keys that a cut
+// splits, the survivors are spread over the group's ids (spread_kept,
+// cx_device.hpp; numpy's argsort leaves which ones unspecified).  A row
+// holding NaN or a negative value is reported as CX_ROW_ERROR and left
+// unwritten.
 __device__ inline void truncate_row(const SampleArgs& A, int row, unsigned char* dyn,
                                     double* red_d, int* red_i) {
   const int t = threadIdx.x;
@@ -770,61 +855,63 @@ __device__ inline void truncate_row(const SampleArgs& A, int row, unsigned char*
     if (t == 0) A.row_status[row] = CX_ROW_ERROR;
     return;
   }
+  __shared__ int s_b1[NWAVE], s_b2[NWAVE];
+  if (t < NWAVE) { s_b1[t] = 0; s_b2[t] = 0; }
   Filters F;
-  F.rank.k = 0;
-  F.rank.i = INT_MAX;
+  F.rank = cut_at(0ull);
   F.floor_p = 0.0;
   F.typ = false;
   F.H = 0.0;
-  F.tcut.k = 0;
-  F.tcut.i = INT_MAX;
+  F.tcut = cut_at(0ull);
+  F.want_tk = false;
+  F.b1 = s_b1;
+  F.b2 = s_b2;
+  __syncthreads();
   const uint64_t kmax = d2key(mx), kmin = d2key(mn);
-  Cut all;
-  all.k = 0;
-  all.i = INT_MAX;
+  const Cut all = cut_at(0ull);
   if (P.top_k > 0 && P.top_k < V) {
     Cut c;
     select_prefix<false, false>(R, F, all, (double)P.top_k, kmin, kmax, L, c, red_d, red_i);
-    F.rank.k = c.k;
-    F.rank.i = INT_MAX;
+    F.rank = cut_at(c.k);
   }
   if (P.top_p < 1.0) {
     Cut c;
     const uint64_t lo = F.rank.k > kmin ? F.rank.k : kmin;
     if (select_prefix<false, true>(R, F, F.rank, P.top_p, lo, kmax, L, c, red_d, red_i))
       F.rank = c;
+    const uint64_t kc = F.rank.k;
+    if (cut_split(F.rank))
+      group_bases(R, F, s_b1, [&](const SElem& e) { return e.key == kc; });
   }
   if (P.min_p > 0.0) F.floor_p = P.min_p * mx;
   if (P.typical_p < 1.0) {
     double h = 0.0;
     uint64_t tlo = ~0ull, thi = 0ull;
-    for (int i = t; i < V; i += WG) {
-      double p = value_at(R, i);
-      if (!kept_rank(F, d2key(p), i, p)) continue;
-      h -= p * log(p > 1e-38 ? p : 1e-38);
-    }
+    visit_row(R, F, [&](const SElem& e) {
+      if (e.kr) h -= e.P * log(e.P > 1e-38 ? e.P : 1e-38);
+    });
     F.H = block_sum(h, red_d);
-    for (int i = t; i < V; i += WG) {
-      double p = value_at(R, i);
-      if (!kept_rank(F, d2key(p), i, p)) continue;
-      uint64_t k = typ_key(p, F.H);
-      tlo = k < tlo ? k : tlo;
-      thi = k > thi ? k : thi;
-    }
+    F.want_tk = true;
+    visit_row(R, F, [&](const SElem& e) {
+      if (e.kr) {
+        tlo = e.tk < tlo ? e.tk : tlo;
+        thi = e.tk > thi ? e.tk : thi;
+      }
+    });
     tlo = block_min<unsigned long long>(tlo, (unsigned long long*)red_d, ~0ull);
     thi = block_max<unsigned long long>(thi, (unsigned long long*)red_d, 0ull);
     Cut c = all;
     if (tlo <= thi)
       F.typ = select_prefix<true, true>(R, F, all, P.typical_p, tlo, thi, L, c, red_d, red_i);
     F.tcut = c;
+    const uint64_t kt = c.k;
+    if (F.typ && cut_split(F.tcut))
+      group_bases(R, F, s_b2, [&](const SElem& e) { return e.kr && e.tk == kt; });
   }
   double* out = A.out64 + (size_t)row * (size_t)A.ldo;
-  for (int i = t; i < V; i += WG) {
-    double p = value_at(R, i);
-    bool keep = kept_rank(F, d2key(p), i, p);
-    if (keep && F.typ) keep = inside(F.tcut, typ_key(p, F.H), i);
-    out[i] = keep ? p : 0.0;
-  }
+  visit_row(R, F, [&](const SElem& e) {
+    if (e.valid) out[e.i] = e.kt ? e.P : 0.0;
+  });
   if (t == 0) A.row_status[row] = CX_ROW_OK;
 }
 

@@ -26,9 +26,15 @@ reference calls it, so the fp64 bits (pairwise ``sum``, sequential ``cumsum``)
 are the reference's bits.
 
 The one freedom is ``argsort`` tie order in S7/S8: numpy's default sort is
-unstable and its tie order depends on the CPU's SIMD sort, so ``tie="numpy"``
-reproduces the reference on this machine and ``tie="stable"`` is the
-documented device rule (equal probabilities: lower token id first).
+unstable and its tie order depends on the SIMD sort numpy dispatches to on
+the CPU at hand, so ``tie="numpy"`` reproduces the reference on this
+machine.  Where a group of equal keys straddles a cut, the order decides
+which members of the group survive; every order keeps the same number of
+them.  ``tie="spread"`` is the device's rule: of a group of n members (in
+ascending id order) of which j survive, the first R members hold
+K(R) = floor((2 R j + n - 1) / (2 n)) survivors, i.e. member r survives iff
+K(r + 1) > K(r) -- the survivors spread evenly over the group's ids.
+``tie="stable"`` (lower id first) is kept for comparison.
 
 Pins (tests/test_oracle_sampler.py):
   * the reference's own known answers, test_sampler.py:7-69;
@@ -120,14 +126,41 @@ def tempered_probs(x: np.ndarray, temperature: float) -> np.ndarray:
 
 
 # --------------------------------------------------------------------- S6-S8
+TIES = ("numpy", "stable", "spread")
+
+
 def _argsort(keys: np.ndarray, tie: str) -> np.ndarray:
-    return np.argsort(keys, kind="stable") if tie == "stable" else np.argsort(keys)
+    if tie not in TIES:
+        raise ValueError(f"tie must be one of {TIES}")
+    return np.argsort(keys) if tie == "numpy" else np.argsort(keys, kind="stable")
+
+
+def spread_kept(R, j: int, n: int):
+    """Survivors among the first R members (ascending id) of a tie group of
+    n members of which j survive a cut: floor((2 R j + n - 1) / (2 n)).
+    Works elementwise on integer arrays."""
+    if j <= 0 or n <= 0:
+        return R * 0
+    if j >= n:
+        return R
+    return (2 * R * j + n - 1) // (2 * n)
+
+
+def spread_mask(n: int, j: int) -> np.ndarray:
+    """Which of the n members (ascending id) of a tie group survive when j do."""
+    r = np.arange(n, dtype=np.int64)
+    return spread_kept(r + 1, j, n) > spread_kept(r, j, n)
 
 
 def _keep_prefix(P: np.ndarray, order: np.ndarray, mass: float, diag: dict,
-                 name: str) -> np.ndarray:
+                 name: str, keys: np.ndarray | None = None,
+                 tie: str = "numpy") -> np.ndarray:
     """Zero everything outside the shortest prefix of ``order`` whose running
-    sum reaches ``mass`` (searchsorted 'left' + 1, sampler.py:84-89)."""
+    sum reaches ``mass`` (searchsorted 'left' + 1, sampler.py:84-89).
+
+    With ``tie="spread"`` (``order`` the stable order of ``keys``), the group
+    of elements whose key equals the last kept element's keeps its survivors
+    by :func:`spread_mask` instead of its lowest ids."""
     run = np.cumsum(P[order])
     m = int(np.searchsorted(run, mass))                       # first run[m] >= mass
     keep = np.zeros(P.shape, dtype=bool)
@@ -138,6 +171,14 @@ def _keep_prefix(P: np.ndarray, order: np.ndarray, mass: float, diag: dict,
         if m + 1 < P.size:
             a, b = P[order[m]], P[order[m + 1]]
             diag[name + "_tie_straddle"] = bool(a == b and a > 0)
+        if tie == "spread" and m + 1 < P.size:
+            ko = keys[order]
+            kc = ko[m]
+            g0 = int(np.searchsorted(ko, kc, side="left"))     # the group's first position
+            g1 = int(np.searchsorted(ko, kc, side="right"))
+            if g1 > m + 1:                                      # the cut splits the group
+                G = order[g0:g1]                                # ascending ids (stable order)
+                keep[G] = spread_mask(g1 - g0, m + 1 - g0)
     return np.where(keep, P, 0.0)
 
 
@@ -151,7 +192,8 @@ def truncate(P: np.ndarray, prm: RowParams, tie: str = "numpy",
         kth = np.partition(out, -k)[-k]
         out = np.where(out >= kth, out, 0.0)
     if prm.top_p < 1.0:                                        # :81-89
-        out = _keep_prefix(out, _argsort(-out, tie), prm.top_p, diag, "top_p")
+        key = -out
+        out = _keep_prefix(out, _argsort(key, tie), prm.top_p, diag, "top_p", key, tie)
     if prm.min_p > 0.0:                                        # :91-93
         floor = prm.min_p * out.max()
         out = np.where(out >= floor, out, 0.0)
@@ -159,7 +201,7 @@ def truncate(P: np.ndarray, prm: RowParams, tie: str = "numpy",
         logp = np.log(np.maximum(out, 1e-38))
         h = -(out * logp).sum()
         dist = np.abs(logp + h)
-        out = _keep_prefix(out, _argsort(dist, tie), prm.typical_p, diag, "typical")
+        out = _keep_prefix(out, _argsort(dist, tie), prm.typical_p, diag, "typical", dist, tie)
     return out
 
 

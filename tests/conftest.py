@@ -42,8 +42,9 @@ def pytest_terminal_summary(terminalreporter, exitstatus, config):
         return
     tr = terminalreporter
     tr.write_line("device vs numpy tie order (reference): label draws differ tie-straddle "
-                  "rate straddling-rows margin-cases")
+                  "rate straddling-rows margin-cases tie-bound")
     for label, r in sorted(rates.items()):
         d = max(r["draws"], 1)
         tr.write_line(f"  {label}: {r['draws']} {r['diff']} {r['diff_tie']} "
-                      f"{r['diff'] / d:.2e} {r['straddle']} {r['margin_vs_stable']}")
+                      f"{r['diff'] / d:.2e} {r['straddle']} {r['margin_vs_spread']} "
+                      f"{r['bound'] if r['bound'] is not None else '1e-4'}")

@@ -38,7 +38,7 @@ def _rows(rng):
     return out
 
 
-def oracle_rows_parallel(w, ties=("stable", "numpy"), keep_probs=False, workers=16) -> list:
+def oracle_rows_parallel(w, ties=("spread", "numpy"), keep_probs=False, workers=16) -> list:
     """[(RowResult per tie order) for every row of SampleWorkload ``w``]."""
     from oracle import sampler_ref as R
     root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))

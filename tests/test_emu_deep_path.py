@@ -130,7 +130,7 @@ def _check(groups, us, out) -> int:
                 assert ids[b] == -2, (kind, b)
                 continue
             assert ids[b] != -2, (kind, b, "handed back")
-            res = R.sample_row(rows[b], prm[b], None, u[b], tie="stable")
+            res = R.sample_row(rows[b], prm[b], None, u[b], tie="spread")
             assert res.status == R.STATUS_OK
             assert int(ids[b]) == res.token, (kind, b, int(ids[b]), res.token)
             decided += 1

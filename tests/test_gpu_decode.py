@@ -37,7 +37,7 @@ def _params(i):
 
 
 def _samplers(seed):
-    ref, dev = OracleSampler(V, tie="stable"), Sampler(V)
+    ref, dev = OracleSampler(V, tie="spread"), Sampler(V)
     ref._rng = np.random.default_rng(seed)
     dev._rng = np.random.default_rng(seed)
     return ref, dev

@@ -46,7 +46,7 @@ def _oracle(x, hists, params):
                          presence_penalty=p.presence_penalty,
                          frequency_penalty=p.frequency_penalty)
         u = np.random.default_rng(p.seed).random()
-        out.append(R.sample_row(x[b], rp, hists[b], u, tie="stable").token)
+        out.append(R.sample_row(x[b], rp, hists[b], u, tie="spread").token)
     return out
 
 
@@ -76,3 +76,30 @@ def test_windows_beyond_one_launch_bf16_device_rows():
     want = _oracle(xb.float().cpu().numpy(), hists, params)
     _say("[gpu] long windows: bf16 device tensor batch")
     assert Sampler(x.shape[1]).sample_batch(xb, params, hists) == want
+
+
+def test_unseeded_rows_after_a_long_window_and_an_argmax_row():
+    """Unseeded rows share the sampler's generator: a row that falls back to
+    argmax (a NaN logit under top-k, sampler.py:123-125) draws nothing, a
+    long-window row takes the separate fp64 launch, and the rows after them
+    take the next variates in order.  Tokens and the generator state after
+    the batch equal the reference's sequential calls."""
+    from oracle_api import OracleSampler
+    rng = np.random.default_rng(5)
+    B, V = 5, 128256
+    x = rng.standard_normal((B, V), dtype=np.float32) * np.float32(2.0)
+    x[0, 17] = np.nan
+    hists = [[], rng.integers(0, V, 10_000).tolist(), [], rng.integers(0, V, 300).tolist(), []]
+    params = [SamplingParams(temperature=1.0, top_k=40),
+              SamplingParams(temperature=0.8, top_p=0.9, repetition_penalty=1.2),
+              SamplingParams(temperature=1.0),
+              SamplingParams(temperature=0.7, top_k=40, repetition_penalty=1.1),
+              SamplingParams(temperature=1.2, top_p=0.95)]
+    dev, ref = Sampler(V), OracleSampler(V, tie="spread")
+    dev._rng = np.random.default_rng(2024)
+    ref._rng = np.random.default_rng(2024)
+    want = [ref.sample(x[b], params[b], hists[b]) for b in range(B)]
+    _say("[gpu] unseeded rows after a long window and an argmax row")
+    got = dev.sample_batch(x, params, hists)
+    assert got == want
+    assert dev._rng.bit_generator.state == ref._rng.bit_generator.state

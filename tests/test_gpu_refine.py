@@ -34,7 +34,7 @@ def _near_cut_rows(rng, x, hist, kw, m_lo, m_hi, rel=1e-9):
         h = None if hist is None else [int(t) for t in hist[b]]
         P = R.tempered_probs(R.penalize(x[b], h, base), base.temperature)
         if base.top_k > 0:
-            P = R.truncate(P, base, tie="stable")
+            P = R.truncate(P, base, tie="spread")
         run = np.cumsum(P[np.argsort(-P, kind="stable")])
         m = int(rng.integers(m_lo, m_hi))
         side = 1.0 if b % 2 else -1.0
@@ -48,7 +48,7 @@ def _check_exact(x, prms, hist, u, want_probs, label):
     _say(f"[gpu] refine {label} B={B} V={x.shape[1]} probs={want_probs}")
     ids, st, probs = sample_host(x, prms, hist, hl, u, want_probs=want_probs)
     orc = [R.sample_row(x[b], prms[b], None if hist is None else [int(t) for t in hist[b]],
-                        float(u[b]), tie="stable", keep_probs=want_probs) for b in range(B)]
+                        float(u[b]), tie="spread", keep_probs=want_probs) for b in range(B)]
     t = compare_rows(ids, st, probs, orc, label)
     assert not t.mismatches, t.mismatches[:5]
     want = np.array([o.token for o in orc])
@@ -130,7 +130,7 @@ def test_tied_group_at_the_cut_takes_the_sorting_finisher(want_probs):
     u = rng.random(B)
     _say(f"[gpu] refine tied group B={B} V={V} probs={want_probs}")
     ids, st, probs = sample_host(x, prms, None, None, u, want_probs=want_probs)
-    orc = [R.sample_row(x[b], prms[b], None, float(u[b]), tie="stable", keep_probs=want_probs)
+    orc = [R.sample_row(x[b], prms[b], None, float(u[b]), tie="spread", keep_probs=want_probs)
            for b in range(B)]
     t = compare_rows(ids, st, probs, orc, "tied group")
     assert not t.mismatches, t.mismatches[:5]

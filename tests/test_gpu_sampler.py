@@ -45,7 +45,7 @@ def _run(w, want_probs=True):
 
 def _check(w, ids, st, probs, label):
     """Device rows against the oracle in both tie orders; returns the tally."""
-    pairs = oracle_rows_parallel(w, ties=("stable", "numpy"), keep_probs=probs is not None)
+    pairs = oracle_rows_parallel(w, ties=("spread", "numpy"), keep_probs=probs is not None)
     t = compare_rows(ids, st, probs, [p[0] for p in pairs], label, ref_rows=[p[1] for p in pairs])
     _say(f"    {label}: draws {t.draws}, margin cases {t.boundary}; vs numpy's order: "
          f"{t.ref_diff} differ ({t.ref_diff_tie} tie straddles), {t.ref_straddle} straddle")
@@ -125,7 +125,7 @@ def test_golden_small_rows():
         u = np.array([np.random.default_rng(c.params["seed"]).random() for c in cs])
         _say(f"[gpu] golden small rows V={V} B={B}")
         ids, st, probs = sample_host(x, prm, hist, hl, u, want_probs=True)
-        orc = [R.sample_row(c.logits, p, c.hist, u[b], tie="stable", keep_probs=True)
+        orc = [R.sample_row(c.logits, p, c.hist, u[b], tie="spread", keep_probs=True)
                for b, (c, p) in enumerate(zip(cs, prm))]
         total.merge(compare_rows(ids, st, probs, orc, f"V{V}"))
     assert not total.mismatches, total.mismatches[:5]
@@ -168,7 +168,7 @@ def test_slow_path_rows():
     u = np.random.default_rng(11).random(B)
     _say(f"[gpu] slow-path rows B={B} V={x.shape[1]}")
     ids, st, probs = sample_host(x, prm, None, None, u, want_probs=True)
-    orc = [R.sample_row(x[b], prm[b], None, u[b], tie="stable", keep_probs=True)
+    orc = [R.sample_row(x[b], prm[b], None, u[b], tie="spread", keep_probs=True)
            for b in range(B)]
     t = compare_rows(ids, st, probs, orc, "slow")
     assert not t.mismatches, t.mismatches[:5]
@@ -192,7 +192,7 @@ def test_penalties_long_window_and_unaligned_rows():
     _say(f"[gpu] penalties B={B} V={V} H={H}")
     ids, st, probs = sample_host(x, prm, hist, hl, u, want_probs=True)
     lists = R.hist_rows_to_lists(hist, hl)
-    orc = [R.sample_row(x[b], prm[b], lists[b], u[b], tie="stable", keep_probs=True)
+    orc = [R.sample_row(x[b], prm[b], lists[b], u[b], tie="spread", keep_probs=True)
            for b in range(B)]
     t = compare_rows(ids, st, probs, orc, "penalties")
     assert not t.mismatches, t.mismatches[:5]

@@ -49,7 +49,8 @@ def test_spec_verify_small_mixed():
     w = W.VerifyWorkload("mixed", tgt, drf, ids, u, T)
     print("[gpu] verify mixed", flush=True)
     acc, nxt, used, st = spec_verify_host(tgt, drf, ids, u, T)
-    _compare(w, acc, nxt, used)
+    # boundary draws within the 1e-4-of-draws budget: none at 48 sequences
+    assert _compare(w, acc, nxt, used) <= 1e-4 * B
 
 
 def test_identical_draft_accepts_everything():
@@ -81,7 +82,7 @@ def test_device_variant_repeated_calls_reuse_the_workspace():
         print(f"[gpu] verify device call {k} B={B} g={g} V={V}", flush=True)
         outs = spec_verify_device(*(torch.from_numpy(a).to(dev) for a in (tgt, drf, ids, u, T)))
         acc, nxt, used, st = (o.cpu().numpy() for o in outs)
-        _compare(W.VerifyWorkload(f"dev{k}", tgt, drf, ids, u, T), acc, nxt, used)
+        assert _compare(W.VerifyWorkload(f"dev{k}", tgt, drf, ids, u, T), acc, nxt, used) <= 1e-4 * B
 
 
 def test_rejections_at_every_position():
@@ -105,5 +106,5 @@ def test_rejections_at_every_position():
     print("[gpu] verify rejection positions", flush=True)
     acc, nxt, used, st = spec_verify_host(tgt, drf, ids, u, T)
     w = W.VerifyWorkload("positions", tgt, drf, ids, u, T)
-    _compare(w, acc, nxt, used)
+    assert _compare(w, acc, nxt, used) <= 1e-4 * B
     assert [int(a) for a in acc] == [min(b % (g + 1), g) for b in range(B)]

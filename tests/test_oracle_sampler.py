@@ -196,6 +196,57 @@ def test_brute_force_topk_and_nucleus():
         assert got == _brute_nucleus_stable(P, p)
 
 
+def test_spread_rule_counts_and_evenness():
+    """spread_mask(n, j) keeps exactly j members, every prefix of R members
+    holds R j / n survivors to within 1/2 (the closest an integer count can
+    be), and j = n / j = 0 keep all / none."""
+    for n in range(1, 40):
+        for j in range(0, n + 1):
+            m = R.spread_mask(n, j)
+            assert int(m.sum()) == j
+            pref = np.concatenate([[0], np.cumsum(m)])
+            R_ = np.arange(n + 1)
+            assert np.all(np.abs(pref - R_ * j / n) <= 0.5 + 1e-12), (n, j)
+            assert np.array_equal(pref, R.spread_kept(R_, j, n))
+    assert R.spread_mask(5, 5).all() and not R.spread_mask(5, 0).any()
+    assert list(np.flatnonzero(R.spread_mask(3, 1))) == [1]        # the middle one
+    assert list(np.flatnonzero(R.spread_mask(4, 2))) == [1, 3]
+
+
+def test_spread_nucleus_against_brute_force():
+    """The spread nucleus keeps every value above the cut value, none below,
+    as many as the stable nucleus, and of the tie group at the cut exactly
+    the spread_mask members (in ascending id order)."""
+    rng = np.random.default_rng(11)
+    straddles = 0
+    for t in range(400):
+        V = int(rng.integers(1, 14))
+        P = np.round(rng.random(V), 1) + 0.05           # ties on purpose
+        P /= P.sum()
+        p = float(rng.choice([0.0, 0.3, 0.5, 0.7, 0.9, 0.999]))
+        ref = _brute_nucleus_stable(P, p)
+        got = set(np.flatnonzero(R.truncate(P, R.RowParams(top_p=p), tie="spread")))
+        assert len(got) == len(ref)
+        vcut = min(P[i] for i in ref)
+        assert {i for i in range(V) if P[i] > vcut} <= got
+        assert not {i for i in got if P[i] < vcut}
+        G = [i for i in range(V) if P[i] == vcut]
+        j = sum(1 for i in ref if P[i] == vcut)
+        assert {G[r] for r in np.flatnonzero(R.spread_mask(len(G), j))} == {i for i in got if P[i] == vcut}
+        straddles += int(j < len(G))
+    assert straddles > 30
+
+
+def test_spread_typical_keeps_the_stable_count():
+    """Typical-p in spread order keeps as many ids, and the same mass, as in
+    the stable order (a flat group straddling the typical cut)."""
+    P = np.array([0.1] * 6 + [0.2, 0.2], dtype=np.float64)
+    for q in (0.15, 0.35, 0.55, 0.75):
+        a = R.truncate(P.copy(), R.RowParams(typical_p=q), tie="stable")
+        b = R.truncate(P.copy(), R.RowParams(typical_p=q), tie="spread")
+        assert (a > 0).sum() == (b > 0).sum() and np.isclose(a.sum(), b.sum())
+
+
 def test_brute_force_draw_distribution():
     """Each id is drawn for exactly the u-interval of width P_i (V <= 6)."""
     rng = np.random.default_rng(3)
@@ -278,3 +329,19 @@ def test_workload_bf16_helper_matches_oracle():
     from chenxing_amd.workloads import f32_to_bf16_rne
     x = np.random.default_rng(1).normal(0, 2, 50000).astype(np.float32)
     assert np.array_equal(f32_to_bf16_rne(x), f32_to_bf16_bits(x))
+
+
+def test_tie_order_fixture_covers_the_bf16_workloads():
+    """tests/golden/tie_order_rates.json (tie_order_rates.py): one entry per
+    bf16 workload the GPU tests bound, and on each the device's order
+    (spread) disagrees with every numpy dispatch level on no more draws than
+    two numpy levels disagree with each other."""
+    import json
+    import os
+    from bf16_workloads import TIE_WORKLOADS
+    path = os.path.join(os.path.dirname(cases.__file__), "tie_order_rates.json")
+    rep = json.load(open(path))
+    assert set(rep["workloads"]) == set(TIE_WORKLOADS)
+    for label, r in rep["workloads"].items():
+        assert r["max_spread_vs_numpy"] <= r["max_numpy_cross_level"], label
+        assert r["draws"] > 0 and r["straddling_rows"] > 0, label

@@ -38,3 +38,26 @@ def test_noalloc_entry_point_matches_the_workspace_entry_point():
         torch.cuda.synchronize()
         assert np.array_equal(ids_a.cpu().numpy(), ids_b.cpu().numpy())
         assert np.array_equal(st_a.cpu().numpy() & 0xFF, st_b.cpu().numpy() & 0xFF)
+
+
+def test_noalloc_entry_point_allocates_nothing():
+    """After a warm-up call, a call of the allocation-free entry point with
+    preallocated outputs leaves both the device's free memory and torch's
+    allocator untouched."""
+    import torch
+    from chenxing_amd import _lib, workloads as W
+    _lib.load()
+    w = W.full_penalty(B=64)
+    print(f"[gpu] noalloc allocation check B={w.B} V={w.V}", flush=True)
+    x, prm, u, h, hl = _batch(w)
+    ids = torch.empty(w.B, dtype=torch.int32, device=x.device)
+    st = torch.empty(w.B, dtype=torch.int32, device=x.device)
+    _lib.sample_device_noalloc(x, prm, u, h, hl, ids, st)       # warm-up
+    torch.cuda.synchronize()
+    free0, _ = torch.cuda.mem_get_info()
+    alloc0 = torch.cuda.memory_allocated()
+    _lib.sample_device_noalloc(x, prm, u, h, hl, ids, st)
+    torch.cuda.synchronize()
+    free1, _ = torch.cuda.mem_get_info()
+    assert torch.cuda.memory_allocated() == alloc0
+    assert free1 == free0
