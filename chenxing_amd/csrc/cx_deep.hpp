@@ -459,7 +459,7 @@ __device__ __forceinline__ bool deep_row_impl(const SampleArgs& A, int row, cons
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int e = 4 * t + j;
-        if (e < g0 || (e < g0 + gn && spread_keeps(e - g0, gj, gn)))
+        if (e < g0 || (e < g0 + gn && spread_keeps(e - g0, gj, gn, V <= TIE_NET)))
           atomicAdd(s_corr + NWAVE + gi[e] / L, (unsigned long long)(qv[j] * fb));
       }
     }
@@ -479,7 +479,7 @@ __device__ __forceinline__ bool deep_row_impl(const SampleArgs& A, int row, cons
       const int mid = (lo + hi) >> 1;
       if (gi[mid] < id) lo = mid + 1; else hi = mid;
     }
-    return spread_keeps(lo - g0, gj, gn);
+    return spread_keeps(lo - g0, gj, gn, V <= TIE_NET);
   };
   auto kept_e = [&](float x, int id, int& amb) -> double {
     const uint32_t kx = f2key(x);

@@ -361,7 +361,7 @@ __device__ inline bool deep16_row_impl(const SampleArgs& A, int row, const cx_ro
   // v*'s kept occurrences in the id ranges: of its cntc occurrences jk are
   // kept, spread over their ids -- the first R hold spread_kept(R) of them
   auto kept_between = [&](int r0, int r1) -> int {
-    return (int)(spread_kept(r1, jk, cntc) - spread_kept(r0, jk, cntc));
+    return (int)(spread_kept(r1, jk, cntc, V <= TIE_NET) - spread_kept(r0, jk, cntc, V <= TIE_NET));
   };
   double Z = 0.0;
   {
@@ -446,7 +446,7 @@ __device__ inline bool deep16_row_impl(const SampleArgs& A, int row, const cx_ro
           if (l >= o) ie += y;
         }
         // occurrences of v* before this lane's, as the spread remainder
-        int rem = spread_rem(bases + eqw + ie - ne, jk, cntc);
+        int rem = spread_rem(bases + eqw + ie - ne, jk, cntc, V <= TIE_NET);
         double q[16];
         double ls = 0.0;
 #pragma unroll
@@ -456,7 +456,7 @@ __device__ inline bool deep16_row_impl(const SampleArgs& A, int row, const cx_ro
             const uint32_t code = deep_code(wd, j);
             const uint32_t key = d16_key(code);
             if (key > kc) v = kept_term(key, code);
-            else if (key == kc) v = spread_step(rem, jk, cntc) ? termc : 0.0;
+            else if (key == kc) v = spread_step(rem, jk, cntc, V <= TIE_NET) ? termc : 0.0;
           }
           q[j] = v;
           ls += v;

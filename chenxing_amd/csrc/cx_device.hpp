@@ -249,38 +249,47 @@ __device__ __forceinline__ void block_argmax(double& v, int& i, double* sv, int*
 
 // ------------------------------------------------------------ tie groups
 // A prefix cut in (key desc, id asc) order that ends inside a group of equal
-// keys keeps j of the group's n members (numpy's argsort, sampler.py:82,103,
-// leaves which ones unspecified).  The survivors are spread evenly over the
-// group's ids: of its first R members (ascending id), spread_kept(R, j, n) =
-// floor((2 R j + n - 1) / (2 n)) survive, so member r survives iff
+// keys keeps j of the group's n members; numpy's argsort (sampler.py:82,103)
+// leaves which ones unspecified, and in practice its choice follows its
+// algorithm: a row of at most TIE_NET entries is sorted by a compare-exchange
+// network, which leaves equal keys mostly in index order, while a longer row
+// is partitioned first, which scatters a group's members.  The device
+// mirrors that: on rows of at most TIE_NET ids (net) the lowest ids of the
+// group survive; on longer rows the survivors are spread evenly over the
+// group's ids -- of its first R members (ascending id), spread_kept(R) =
+// floor((2 R j + n - 1) / (2 n)) survive.  Either way member r survives iff
 // spread_kept(r + 1) > spread_kept(r), and the members of an id range
-// [R0, R1) hold spread_kept(R1) - spread_kept(R0) survivors.  (Lower ids
-// first would keep the group's lowest ids: a systematic bias of the draw
-// towards low ids that numpy's unstable orders do not have.)
+// [R0, R1) hold spread_kept(R1) - spread_kept(R0) survivors.  (Lowest ids on
+// long rows would bias the draw towards low ids at every split group.)
+constexpr int TIE_NET = 256;
 // (Group sizes are below 2^21, so x = 2 R j + n - 1 < 2^43 is exact in fp64,
 // and so is floor(x / 2n) of the correctly rounded quotient: a quotient below
 // an integer lies at least 1 / 2n below it, far more than its rounding error
 // for x < 2^53.  A 64-bit integer division would expand into a long, register
 // hungry sequence at every use.)
-__device__ __forceinline__ long long spread_kept(long long R, long long j, long long n) {
+__device__ __forceinline__ long long spread_kept(long long R, long long j, long long n, bool net) {
   if (j <= 0 || n <= 0) return 0;
   if (j >= n) return R;
+  if (net) return R < j ? R : j;
   const double x = (double)(2 * R * j + n - 1);
   return (long long)floor(x / (double)(2 * n));
 }
-__device__ __forceinline__ bool spread_keeps(long long r, long long j, long long n) {
-  return spread_kept(r + 1, j, n) > spread_kept(r, j, n);
+__device__ __forceinline__ bool spread_keeps(long long r, long long j, long long n, bool net) {
+  return spread_kept(r + 1, j, n, net) > spread_kept(r, j, n, net);
 }
-// The same decision for consecutive members without a division each: with
-// x_r = 2 r j + n - 1, member r survives iff (x_r mod 2n) + 2j >= 2n, and
-// x_{r+1} mod 2n follows by one addition.  spread_rem gives x_r mod 2n (n >
-// 0); spread_step decides member r from it and advances it to r + 1.
-__device__ __forceinline__ int spread_rem(long long r, long long j, long long n) {
+// The same decision for consecutive members without a division each.  On
+// long rows, with x_r = 2 r j + n - 1, member r survives iff (x_r mod 2n) +
+// 2j >= 2n, and x_{r+1} mod 2n follows by one addition; on net rows the
+// state is the rank itself.  spread_rem gives the state of member r;
+// spread_step decides member r from it and advances it to r + 1.
+__device__ __forceinline__ int spread_rem(long long r, long long j, long long n, bool net) {
+  if (net) return (int)r;
   if (n <= 0) return 0;
   const double x = (double)(2 * r * j + n - 1), d = (double)(2 * n);
   return (int)(x - floor(x / d) * d);
 }
-__device__ __forceinline__ bool spread_step(int& rem, int j, int n) {
+__device__ __forceinline__ bool spread_step(int& rem, int j, int n, bool net) {
+  if (net) return rem++ < j;
   const bool keep = rem + 2 * j >= 2 * n;
   rem += 2 * j;
   rem -= rem >= 2 * n ? 2 * n : 0;

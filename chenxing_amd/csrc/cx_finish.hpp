@@ -288,7 +288,8 @@ __device__ inline int finish_bucketed(const SampleArgs& A, int row, const cx_row
         if (kf[j] && vbucket(j) >= bc) kf[j] = 0;
       __syncthreads();
       // the cut bucket's entries before the cut value, and its group's survivors
-      if (t < g0 || (t < g1 && spread_keeps(t - g0, pos + 1 - g0, g1 - g0))) kf[ga[t]] = 1;
+      if (t < g0 || (t < g1 && spread_keeps(t - g0, pos + 1 - g0, g1 - g0, A.V <= TIE_NET)))
+        kf[ga[t]] = 1;
       __syncthreads();
       complete = true;
     } else {
@@ -531,8 +532,8 @@ __device__ inline int finish_row_fast(const SampleArgs& A, int row, const cx_row
 #pragma unroll
         for (int q = 0; q < R; ++q) {
           const int r = q * WG + t;
-          if (r < ng && spread_keeps(r, jg, ng)) {
-            const int d = g0 + (int)spread_kept(r, jg, ng);
+          if (r < ng && spread_keeps(r, jg, ng, A.V <= TIE_NET)) {
+            const int d = g0 + (int)spread_kept(r, jg, ng, A.V <= TIE_NET);
             skey[d] = mk[q];
             sidx[d] = mi[q];
           }

@@ -783,7 +783,8 @@ constexpr int LEAN_NEAR = 2;     // a top-p cut within the normaliser's error bo
 
 __device__ inline int lean_decide(const cx_row_params& P, const CX_LDS uint64_t* gk,
                                   const CX_LDS int32_t* gi, int nlist, double kc, double Rb,
-                                  double S, double tol, CX_LDS LeanLds* L, double u, int& tok) {
+                                  double S, double tol, CX_LDS LeanLds* L, double u, bool net,
+                                  int& tok) {
   const int l = lane_id();
   // the top 65 entries in value order, and every id at its id rank
   for (int e = l; e < nlist; e += 64) {
@@ -824,7 +825,7 @@ __device__ inline int lean_decide(const cx_row_params& P, const CX_LDS uint64_t*
       const uint64_t kcut = lane_read(key, mm);
       const uint64_t g = ballot(l < n && key == kcut);
       const int g0 = __builtin_ctzll(g), g1 = 64 - __builtin_clzll(g);
-      keep = l < g0 || (l < g1 && spread_keeps(l - g0, mm + 1 - g0, g1 - g0));
+      keep = l < g0 || (l < g1 && spread_keeps(l - g0, mm + 1 - g0, g1 - g0, net));
     } else {
       const double cl = lane_read(cum, n - 1);
       near = fabs(cl - P.top_p) <= tol * cl;
@@ -1307,7 +1308,8 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
     __syncthreads();
     if (wave_id() != 0) return;
     int tok = -1;
-    const int dr = ok ? lean_decide(P, lgk, lgi, nlist, kc, Rb, Ss, tol, L, u_row, tok)
+    const int dr = ok ? lean_decide(P, lgk, lgi, nlist, kc, Rb, Ss, tol, L, u_row,
+                                    A.V <= TIE_NET, tok)
                       : LEAN_PENDING;
     if (dr == LEAN_NEAR) {
       // the list as the row's region (every element at or above the largest

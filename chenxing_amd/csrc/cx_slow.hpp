@@ -120,24 +120,26 @@ __device__ __forceinline__ double mass_of(const SlowRow& R, double v) {
 
 // Boundary of a prefix in (key desc, idx asc) order over the eligible
 // elements: keys above k are inside, keys below outside; of the n eligible
-// elements whose key equals k, j are inside, spread over their ids -- the
-// one of rank r (members with a lower id before it) is inside iff
-// spread_keeps(r, j, n) (cx_device.hpp).  j >= n: the whole group is inside
+// elements whose key equals k, j are inside, spread over their ids (on rows
+// of at most TIE_NET ids, its lowest ids) -- the one of rank r (members with
+// a lower id before it) is inside iff spread_keeps(r, j, n) (cx_device.hpp).  j >= n: the whole group is inside
 // (top-k keeps its ties, and a cut that ends a group splits nothing).
 struct Cut {
   uint64_t k;
   int n, j;
+  bool net;          // a row of at most TIE_NET ids: the lowest ids survive
 };
 __device__ __forceinline__ Cut cut_at(uint64_t k) {
   Cut c;
   c.k = k;
   c.n = 0;
   c.j = 0;
+  c.net = false;
   return c;
 }
 __device__ __forceinline__ bool cut_split(const Cut& c) { return c.j < c.n; }
 __device__ __forceinline__ bool inside(const Cut& c, uint64_t key, int rank) {
-  return key > c.k || (key == c.k && (c.j >= c.n || spread_keeps(rank, c.j, c.n)));
+  return key > c.k || (key == c.k && (c.j >= c.n || spread_keeps(rank, c.j, c.n, c.net)));
 }
 
 struct Filters {
@@ -326,6 +328,7 @@ __device__ __forceinline__ bool select_prefix(const SlowRow& R, const Filters& F
       out.k = klo;
       out.n = nb;
       out.j = sh_i[2];
+      out.net = R.V <= TIE_NET;
       __syncthreads();
       return true;
     }
@@ -370,6 +373,7 @@ __device__ __forceinline__ bool select_prefix(const SlowRow& R, const Filters& F
       out.k = sh_u[0];
       out.n = sh_i[0];
       out.j = sh_i[1];
+      out.net = R.V <= TIE_NET;
       __syncthreads();
       return true;
     }
@@ -476,6 +480,7 @@ __device__ __forceinline__ bool select_mass_linear(const SlowRow& R, double targ
       out.k = kj;
       out.n = g1 - g0;
       out.j = j + 1 - g0;
+      out.net = R.V <= TIE_NET;
       __syncthreads();
       return true;
     }

@@ -30,11 +30,15 @@ unstable and its tie order depends on the SIMD sort numpy dispatches to on
 the CPU at hand, so ``tie="numpy"`` reproduces the reference on this
 machine.  Where a group of equal keys straddles a cut, the order decides
 which members of the group survive; every order keeps the same number of
-them.  ``tie="spread"`` is the device's rule: of a group of n members (in
-ascending id order) of which j survive, the first R members hold
-K(R) = floor((2 R j + n - 1) / (2 n)) survivors, i.e. member r survives iff
-K(r + 1) > K(r) -- the survivors spread evenly over the group's ids.
-``tie="stable"`` (lower id first) is kept for comparison.
+them.  ``tie="spread"`` is the device's rule, which follows how numpy's
+SIMD argsort treats ties: a row of at most TIE_NET (256) entries is sorted
+by a compare-exchange network that leaves equal keys mostly in index order,
+so there the group's lowest ids survive; on a longer row, which numpy
+partitions first, the survivors spread evenly over the group's ids -- of a
+group of n members (in ascending id order) of which j survive, the first R
+members hold K(R) = floor((2 R j + n - 1) / (2 n)) survivors, i.e. member r
+survives iff K(r + 1) > K(r).  ``tie="stable"`` (lower id first on every
+row) is kept for comparison.
 
 Pins (tests/test_oracle_sampler.py):
   * the reference's own known answers, test_sampler.py:7-69;
@@ -127,6 +131,7 @@ def tempered_probs(x: np.ndarray, temperature: float) -> np.ndarray:
 
 # --------------------------------------------------------------------- S6-S8
 TIES = ("numpy", "stable", "spread")
+TIE_NET = 256        # rows up to this length keep a split group's lowest ids
 
 
 def _argsort(keys: np.ndarray, tie: str) -> np.ndarray:
@@ -158,9 +163,10 @@ def _keep_prefix(P: np.ndarray, order: np.ndarray, mass: float, diag: dict,
     """Zero everything outside the shortest prefix of ``order`` whose running
     sum reaches ``mass`` (searchsorted 'left' + 1, sampler.py:84-89).
 
-    With ``tie="spread"`` (``order`` the stable order of ``keys``), the group
-    of elements whose key equals the last kept element's keeps its survivors
-    by :func:`spread_mask` instead of its lowest ids."""
+    With ``tie="spread"`` (``order`` the stable order of ``keys``) on a row
+    longer than TIE_NET, the group of elements whose key equals the last kept
+    element's keeps its survivors by :func:`spread_mask` instead of its
+    lowest ids."""
     run = np.cumsum(P[order])
     m = int(np.searchsorted(run, mass))                       # first run[m] >= mass
     keep = np.zeros(P.shape, dtype=bool)
@@ -171,7 +177,7 @@ def _keep_prefix(P: np.ndarray, order: np.ndarray, mass: float, diag: dict,
         if m + 1 < P.size:
             a, b = P[order[m]], P[order[m + 1]]
             diag[name + "_tie_straddle"] = bool(a == b and a > 0)
-        if tie == "spread" and m + 1 < P.size:
+        if tie == "spread" and m + 1 < P.size and P.size > TIE_NET:
             ko = keys[order]
             kc = ko[m]
             g0 = int(np.searchsorted(ko, kc, side="left"))     # the group's first position

@@ -214,18 +214,22 @@ def test_spread_rule_counts_and_evenness():
 
 
 def test_spread_nucleus_against_brute_force():
-    """The spread nucleus keeps every value above the cut value, none below,
-    as many as the stable nucleus, and of the tie group at the cut exactly
-    the spread_mask members (in ascending id order)."""
+    """On rows longer than TIE_NET the spread nucleus keeps every value
+    above the cut value, none below, as many as the stable nucleus, and of
+    the tie group at the cut exactly the spread_mask members (in ascending
+    id order); on rows of at most TIE_NET it is the stable nucleus."""
     rng = np.random.default_rng(11)
     straddles = 0
-    for t in range(400):
-        V = int(rng.integers(1, 14))
+    for t in range(120):
+        V = int(rng.choice([5, 40, R.TIE_NET, R.TIE_NET + 1, 300, 700]))
         P = np.round(rng.random(V), 1) + 0.05           # ties on purpose
         P /= P.sum()
         p = float(rng.choice([0.0, 0.3, 0.5, 0.7, 0.9, 0.999]))
         ref = _brute_nucleus_stable(P, p)
         got = set(np.flatnonzero(R.truncate(P, R.RowParams(top_p=p), tie="spread")))
+        if V <= R.TIE_NET:
+            assert got == ref
+            continue
         assert len(got) == len(ref)
         vcut = min(P[i] for i in ref)
         assert {i for i in range(V) if P[i] > vcut} <= got
@@ -234,13 +238,13 @@ def test_spread_nucleus_against_brute_force():
         j = sum(1 for i in ref if P[i] == vcut)
         assert {G[r] for r in np.flatnonzero(R.spread_mask(len(G), j))} == {i for i in got if P[i] == vcut}
         straddles += int(j < len(G))
-    assert straddles > 30
+    assert straddles > 20
 
 
 def test_spread_typical_keeps_the_stable_count():
     """Typical-p in spread order keeps as many ids, and the same mass, as in
     the stable order (a flat group straddling the typical cut)."""
-    P = np.array([0.1] * 6 + [0.2, 0.2], dtype=np.float64)
+    P = np.array([0.1] * 6 + [0.2, 0.2] + [0.0] * 300, dtype=np.float64)
     for q in (0.15, 0.35, 0.55, 0.75):
         a = R.truncate(P.copy(), R.RowParams(typical_p=q), tie="stable")
         b = R.truncate(P.copy(), R.RowParams(typical_p=q), tie="spread")
