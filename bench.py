@@ -18,7 +18,7 @@ already resident in HBM.  A step is one cx_sample_f32 call over the batch.
                of the same rows (reported beside, not a target); also a
                process pool of up to 16 workers (cpu_baseline_pool)
 
-The other workloads (nucleus, speculative verify, heterogeneous bf16) are
+The other workloads (nucleus, typical-p, speculative verify, heterogeneous bf16) are
 timed the same way and reported under "other_workloads"; "host_calls" times
 the drop-in Sampler on numpy rows as the reference's engine calls it
 (copies to and from the device included).
@@ -222,6 +222,7 @@ def cpu_baseline_pool(w, rows_per_worker: int, workers: int) -> dict:
 OTHER = {  # name: (workload factory, kernel whose launches are timed)
     "nucleus": ("nucleus", {}, 0),
     "nucleus_greedy": ("nucleus", {"greedy": True}, 0),
+    "typical": ("typical", {}, 0),
     "hetero_bf16": ("hetero_bf16", {}, 0),
     "spec_verify": ("spec_verify", {}, 2),
     "spec_verify_greedy": ("spec_verify", {"greedy": True}, 2),

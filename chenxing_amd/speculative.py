@@ -100,8 +100,15 @@ class SpeculativeDecoder:
         q_rows.append(self.draft.forward_ids(dseq, [confirmed[n_start]],
                                              allow_unconfirmed=True)[-1])
         for i in range(self.k_draft):
-            tok = self.draft.sampler.sample(q_rows[-1], _GREEDY) if greedy else \
-                self.draft.sampler.sample(q_rows[-1], params, confirmed)
+            row = q_rows[-1]
+            if greedy and isinstance(row, np.ndarray):
+                # a host row: the reference's own argmax (speculative.py:125),
+                # no device round trip for one id
+                tok = int(np.argmax(row))
+            elif greedy:
+                tok = self.draft.sampler.sample(row, _GREEDY)
+            else:
+                tok = self.draft.sampler.sample(row, params, confirmed)
             proposed.append(tok)
             self.stats.drafted += 1
             if i < self.k_draft - 1:

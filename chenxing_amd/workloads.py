@@ -14,6 +14,8 @@ deviation s.  Sizes:
   spec_verify     B=32, gamma=8, V=128256: target N(0,2) [B, 9, V], draft =
                   target[:, :8] + N(0, 0.5); draft ids drawn from the draft
                   softmax; T 1.0 or greedy
+  typical         the nucleus logits, T 1.0, typical-p 0.95 (the exact
+                  multi-pass path)
   hetero_bf16     B=1024, V=256000, bf16 of N(0,2) + 10 on 3 ids/row; per-row
                   T ~ U[0.3, 1.5], top-k in {0, 20, 100, 1000},
                   top-p ~ U[0.5, 1.0], 25% of rows greedy
@@ -90,6 +92,14 @@ def nucleus(seed: int = 0, B: int = 64, V: int = 128256, greedy: bool = False) -
     u = np.random.default_rng(seed + 1).random(B)
     return SampleWorkload("nucleus_greedy" if greedy else "nucleus", x, "f32", [prm] * B,
                           np.zeros((B, 0), np.int32), np.zeros(B, np.int32), u)
+
+
+def typical(seed: int = 0, B: int = 64, V: int = 128256, typical_p: float = 0.95) -> SampleWorkload:
+    """The nucleus logits with typical-p sampling (sampler.py:95-105): T 1.0,
+    typical_p 0.95, no other filter, no penalties."""
+    w = nucleus(seed, B, V)
+    prm = RowParams(temperature=1.0, typical_p=typical_p)
+    return SampleWorkload("typical", w.logits, "f32", [prm] * B, w.hist, w.hist_len, w.u)
 
 
 def zipf_history(rng: np.random.Generator, B: int, H: int, V: int) -> np.ndarray:
