@@ -335,8 +335,10 @@ __device__ inline int finish_bucketed(const SampleArgs& A, int row, const cx_row
 
 // Finish a row from its region (at most CAP entries, CAP / WG per thread).
 // S_exact > 0 is the exact fp64 normaliser sum exp((x - M) / T) over the
-// row, replacing the slices' streamed sums; the top-p cut is then taken as
-// it falls.  Nothing is written unless the outcome is FIN_DONE.
+// row, replacing the slices' streamed sums; so is the sum of the slices'
+// own exact fp64 sums when every slice recorded one (SF_EXACT).  With an
+// exact normaliser the top-p cut is taken as it falls.  Nothing is written
+// unless the outcome is FIN_DONE.
 template <int CAP>
 __device__ inline int finish_row_fast(const SampleArgs& A, int row, const cx_row_params& P,
                                       unsigned char* dyn, double* red_d, int* red_i,
@@ -383,8 +385,23 @@ __device__ inline int finish_row_fast(const SampleArgs& A, int row, const cx_row
     tau = max(tau, st[s].tau);
     tol = st[s].tol > tol ? st[s].tol : tol;
   }
-  const bool exact = S_exact > 0.0;
-  if (exact) S = S_exact;
+  bool exact = S_exact > 0.0;
+  if (exact) {
+    S = S_exact;
+  } else if (flags & SF_EXACT) {
+    // the slices' exact fp64 sums (sliced top-p rows), when every slice has
+    // one: S = sum over slices of sx_s exp((m_s - M) / T)
+    bool allx = true;
+    double Sx = 0.0;
+    for (int s = 0; s < nsp; ++s) {
+      allx = allx && (st[s].flags & SF_EXACT);
+      if ((st[s].flags & SF_EXACT) && st[s].sx != 0.0) Sx += st[s].sx * exp((st[s].m - M) * invT);
+    }
+    if (allx && Sx > 0.0 && Sx < __builtin_inf()) {
+      S = Sx;
+      exact = true;
+    }
+  }
   // Degenerate rows (NaN / +inf / all -inf), tie floods, typical-p and a
   // possible P**(1/T) underflow (ln V / T > 740) go to the multi-pass kernel.
   if (mnan || !(S > 0.0) || !(S < __builtin_inf()) ||

@@ -21,6 +21,7 @@ constexpr double TOL_MAX = 1e-4;          // rows whose bound exceeds this are r
 constexpr int SF_OVERFLOW = 1;            // a wave buffer flooded with ties
 constexpr int SF_UNSUPPORTED = 2;         // window longer than WIN_MAX
 constexpr int SF_INEXACT = 4;             // the slice's normaliser has no usable error bound
+constexpr int SF_EXACT = 8;               // sx holds the slice's exact fp64 normaliser
 
 
 // Internal row_status values, never returned to the caller, for slow_kernel:
@@ -50,7 +51,8 @@ struct SplitStats {       // one per (row, slice), 64 bytes
   int32_t ncand;          // region entries written to the workspace
   int32_t flags;
   int32_t pad1;
-  double xshare;          // slow_kernel: this part's share of the row's exact normaliser
+  double sx;              // with SF_EXACT: sum of exp((x - m) / T) over the slice in fp64
+                          // (each term within 1 ulp; sliced top-p rows)
 };
 static_assert(sizeof(SplitStats) == 64, "SplitStats layout");
 
@@ -73,8 +75,8 @@ struct SampleArgs {
   int32_t* row_status;
   float* out_probs;
   // [B + 1], each written by the fused kernel before the later kernels read
-  // it: [row] of a sliced row, its exact-normaliser shares summed (zeroed);
-  // [row] of a single-slice row, its hand-off mark (ROW_FINISH, ROW_REFINE,
+  // it: [row] of a sliced row, 0; [row] of a single-slice row, its hand-off
+  // mark (ROW_FINISH, ROW_REFINE,
   // ROW_PENDING, or 0 if decided, with MARK_DEEP and MARK_TOPK), which,
   // unlike row_status, the finishing kernels leave as it is; [B],
   // finish16_kernel's work-item counter (zeroed)
@@ -96,9 +98,6 @@ struct SampleArgs {
   int32_t slow_off_hkey, slow_off_work, slow_off_tsum, slow_lds_bytes;
   // slow_kernel takes only rows marked ROW_PENDING (after finish16_kernel)
   int32_t pending_only;
-  // slow_kernel's grid is B * nsplit: the workgroups of a sliced top-p row
-  // each sum a share of its exact normaliser, the last to finish takes the row
-  int32_t par_exact;
 };
 
 // ---------------------------------------------------------------- verify

@@ -555,14 +555,30 @@ __device__ __forceinline__ void append_chunk(WaveBuf& wb,
 // loop alternates between the two buffers (no register copies, which would
 // wait for the chunk still in flight): it consumes one and refills it with
 // the chunk after the other, so two chunks stay in flight.
-template <bool BF16>
+// An exact fp64 running sum of exp((x - m) / T) over one lane's elements,
+// against m, the largest value the lane has seen (rescaled by exp((m_old -
+// m) / T) when m rises): each term within 1 ulp (exp64_neg).  Kept only by
+// the sliced-launch kernel, for stochastic top-p rows, so that the row's
+// exact normaliser needs no second read of the row.
+struct XSum {
+  double s, m;
+};
+__device__ __forceinline__ void xsum_raise(XSum& xs, double cm, double invT, const double* etab) {
+  if (cm > xs.m) {
+    if (xs.s != 0.0) xs.s *= exp64_neg((xs.m - cm) * invT, etab);
+    xs.m = cm;
+  }
+}
+
+template <bool BF16, bool EXACT>
 __device__ __forceinline__ void stream_stoch(__amdgpu_buffer_rsrc_t rs,
                                              typename Elem<BF16>::V (&q)[Elem<BF16>::U],
                                              typename Elem<BF16>::V (&qn)[Elem<BF16>::U], int nv,
                                              int lo, bool pen_on, const PenIndex& X, float c,
                                              int krow, int pub_r, CX_LDS int* chunk_ctr,
                                              CX_LDS uint32_t* slots, CX_LDS uint32_t* w_pub,
-                                             SState& st, WaveBuf& wb, uint32_t& ck) {
+                                             SState& st, WaveBuf& wb, uint32_t& ck, bool ex,
+                                             double invT, const double* etab, XSum& xs) {
   using E = Elem<BF16>;
   using V = typename E::V;
   constexpr int NE = E::NE;
@@ -605,6 +621,18 @@ __device__ __forceinline__ void stream_stoch(__amdgpu_buffer_rsrc_t rs,
     // other than the buffer's, and the loop's back edge copies them over
     // after waiting for every load in flight.
     __asm__ volatile("" : "+v"(st.s));
+    if (EXACT && ex) {
+      xsum_raise(xs, (double)cmax, invT, etab);
+      if (xs.m > -__builtin_inf()) {
+        double a = 0.0;
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+          for (int j = 0; j < NE; ++j) a += exp64_neg(((double)x[u][j] - xs.m) * invT, etab);
+        xs.s += a;
+      }
+      __asm__ volatile("" : "+v"(xs.s));
+    }
     const bool flagged = cmax >= wb.tauf;
     if (ballot(flagged)) {
       append_chunk<BF16>(wb, x, flagged, vb, nv, lo, pen_on, X, share, ck);
@@ -632,10 +660,11 @@ __device__ __forceinline__ void stream_stoch(__amdgpu_buffer_rsrc_t rs,
 
 // Scalar elements [s0, hi) of a stochastic slice (unaligned rows, or the
 // tail after the last whole vector).
-template <bool BF16>
+template <bool BF16, bool EXACT>
 __device__ __forceinline__ void stream_scalar(const char* rowp, int s0, int lo, int hi,
                                               bool pen_on, const PenIndex& X, float c, bool share,
-                                              SState& st, WaveBuf& wb, uint32_t& ck) {
+                                              SState& st, WaveBuf& wb, uint32_t& ck, bool ex,
+                                              double invT, const double* etab, XSum& xs) {
   using E = Elem<BF16>;
   const float lim = LIM / c;
   for (int e = s0 + lane_id() + 64 * wave_id(); e - lane_id() < hi; e += WG) {
@@ -643,6 +672,10 @@ __device__ __forceinline__ void stream_scalar(const char* rowp, int s0, int lo, 
     const float x = valid ? E::scalar(rowp, e) : -__builtin_inff();
     rescale(x, c, lim, st);
     st.s += (double)__builtin_amdgcn_exp2f(__builtin_fmaf(x, c, st.nR));
+    if (EXACT && ex) {
+      xsum_raise(xs, (double)x, invT, etab);
+      if (xs.m > -__builtin_inf()) xs.s += exp64_neg(((double)x - xs.m) * invT, etab);
+    }
     uint32_t k = 0u;
     if (valid && x >= wb.tauf && !(pen_on && pen_bit(X, e - lo))) k = f2key(x);
     if (ballot(k != 0u)) {
@@ -873,6 +906,7 @@ __device__ inline int lean_decide(const cx_row_params& P, const CX_LDS uint64_t*
 // <= 1), and the largest penalised value.
 struct PenRec {
   double corr, pr, pmx, Rc;
+  double corrx, prx, refx;   // fp64 exact: penalised-minus-raw and raw terms against refx
   int fl, pad;
 };
 
@@ -895,12 +929,14 @@ __device__ __forceinline__ int next_group(CX_LDS int* ctr, int ngroups) {
 // ceil(max * c), rescaled exactly when it rises), the raw terms (pr) and
 // the penalised-minus-raw terms (corr): fp32 terms each <= 1 and within
 // TOL_T of the exact ones.
-template <bool BF16>
+template <bool BF16, bool EXACT>
 __device__ __forceinline__ void pen_correct(const PenIndex& X, int nd, CX_LDS int* gctr,
                                             const char* rowp, const cx_row_params& P, double kc,
                                             double thr_w, CX_LDS uint64_t* lgk,
-                                            CX_LDS int32_t* lgi, CX_LDS int* lcnt, PenRec* rec) {
+                                            CX_LDS int32_t* lgi, CX_LDS int* lcnt, PenRec* rec,
+                                            bool ex, double invT, const double* etab) {
   double corr = 0.0, pr = 0.0, pmx = -__builtin_inf(), Rc = 0.0;
+  XSum cx{0.0, -__builtin_inf()}, px{0.0, -__builtin_inf()};
   int fl = 0;
   bool any = false;
   const int ngroups = (nd + 63) >> 6;
@@ -943,14 +979,31 @@ __device__ __forceinline__ void pen_correct(const PenIndex& X, int nd, CX_LDS in
     }
     corr += wave_reduce(tp - tr, OpAdd());
     pr += wave_reduce(tr, OpAdd());
+    if (EXACT && ex && pm > -__builtin_inf() && pm < __builtin_inf()) {
+      // the same in fp64 against the running maximum pm
+      xsum_raise(cx, pm, invT, etab);
+      xsum_raise(px, pm, invT, etab);
+      double tpx = 0.0, trx = 0.0;
+      if (v && xp == xp) {
+        tpx = exp64_neg((xp - cx.m) * invT, etab);
+        trx = exp64_neg(((double)raw - cx.m) * invT, etab);
+      }
+      cx.s += wave_reduce(tpx - trx, OpAdd());
+      px.s += wave_reduce(trx, OpAdd());
+    }
   }
   pmx = wave_reduce(pmx, OpMax());
   fl = wave_reduce(fl, OpOr());
-  if (lane_id() == 0) { rec->corr = corr; rec->pr = pr; rec->pmx = pmx; rec->Rc = Rc; rec->fl = fl; }
+  if (lane_id() == 0) {
+    rec->corr = corr; rec->pr = pr; rec->pmx = pmx; rec->Rc = Rc; rec->fl = fl;
+    rec->corrx = cx.s; rec->prx = px.s; rec->refx = cx.m;
+  }
 }
 
 // ------------------------------------------------------------ the kernel
-template <bool BF16>
+// EXACT: the kernel of sliced launches (nsplit > 1), whose stochastic top-p
+// rows also keep the exact fp64 normaliser of each slice (XSum).
+template <bool BF16, bool EXACT>
 __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   using E = Elem<BF16>;
   constexpr int NE = E::NE;
@@ -974,6 +1027,8 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
 
   __shared__ int s_nd;
   __shared__ int s_gctr;
+  __shared__ double s_etab[EXACT ? 64 : 1];   // EXP64_TAB, for the exact sums
+  __shared__ double w_xs[EXACT ? NWAVE : 1], w_xm[EXACT ? NWAVE : 1];
   const int row = blockIdx.x / A.nsplit;
   const int split = blockIdx.x % A.nsplit;
   const int t = threadIdx.x;
@@ -1008,10 +1063,9 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   const int ch0 = __builtin_amdgcn_readfirstlane(wave_id());
   typename E::V q[U], qn[U];
   load_chunk<BF16>(rs, ch0, q);
-  // slow_kernel's count of a sliced row's exact-normaliser shares starts at
+  // a row's hand-off mark and finish16_kernel's work-item counter start at
   // zero (the workspace may hold a previous call's records of another
-  // layout), as do a single-slice row's hand-off mark and finish16_kernel's
-  // work-item counter
+  // layout)
   if (split == 0 && t == 0) A.counters[row] = 0;
   if (blockIdx.x == 0 && t == 0) A.counters[A.B] = 0;
 
@@ -1052,6 +1106,7 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   if (t < LEAN_CAP) { s_lean.rv[t] = 0; s_lean.ri[t] = 0; }
   if (t < NWAVE) { w_pub[t] = 0u; w_cnt[t] = 0; }
   if (t < 4 * NWAVE) slots[t] = 0u;
+  if (EXACT && t < 64) s_etab[t] = EXP64_TAB[t];
   if (pen_on) {
     for (int i = t; i < X.nbw; i += WG) X.bitmap[i] = 0u;
     for (int i = t; i < X.ns; i += WG) X.hword[i] = HW_EMPTY;
@@ -1139,6 +1194,12 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   // ---------------------------------------------------------------- stochastic
   const float c = (float)(1.4426950408889634 / P.temperature);
   const double kc = (double)c;
+  // the exact fp64 slice normaliser: sliced top-p rows, whose cut the
+  // finisher otherwise could only refine with a second read of the row
+  const bool ex = EXACT && P.top_p < 1.0;
+  const double invT = 1.0 / P.temperature;
+  const double* etab = EXACT ? (const double*)s_etab : nullptr;
+  XSum xs{0.0, -__builtin_inf()};
   WaveBuf wb;
   wb.key = to_lds((uint32_t*)(dyn + A.off_wkey) + wave_id() * CAPW);
   wb.idx = to_lds((int32_t*)(dyn + A.off_widx) + wave_id() * CAPW);
@@ -1223,11 +1284,12 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   CX_LDS uint64_t* const lgk = to_lds(gk);
   CX_LDS int32_t* const lgi = to_lds(gi);
   CX_LDS int* const lcnt = to_lds(&s_cnt);
-  stream_stoch<BF16>(rs, q, qn, nv, lo, pen_on, X, c, krow, pub_r, to_lds(&s_chunk), lslots,
-                     lpub, st, wb, ck);
+  stream_stoch<BF16, EXACT>(rs, q, qn, nv, lo, pen_on, X, c, krow, pub_r, to_lds(&s_chunk),
+                            lslots, lpub, st, wb, ck, ex, invT, etab, xs);
   if (s0 < hi) {
     raise_tau(wb, lds_load(wb.shared));
-    stream_scalar<BF16>(rowp, s0, lo, hi, pen_on, X, c, true, st, wb, ck);
+    stream_scalar<BF16, EXACT>(rowp, s0, lo, hi, pen_on, X, c, true, st, wb, ck, ex, invT, etab,
+                               xs);
   }
 
   // ---- per wave, after its stream: its region entries into the shared
@@ -1245,11 +1307,21 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
     }
   }
   if (pen_on) {
-    pen_correct<BF16>(X, nd, gctr, rowp, P, kc, wb.tau <= 1u ? -__builtin_inf() : (double)wb.tauf,
-                      lgk, lgi, lcnt, &s_pen[wave_id()]);
+    pen_correct<BF16, EXACT>(X, nd, gctr, rowp, P, kc,
+                             wb.tau <= 1u ? -__builtin_inf() : (double)wb.tauf, lgk, lgi, lcnt,
+                             &s_pen[wave_id()], ex, invT, etab);
   } else if (lane_id() == 0) {
     s_pen[wave_id()].corr = 0.0; s_pen[wave_id()].pr = 0.0; s_pen[wave_id()].pmx = -__builtin_inf();
     s_pen[wave_id()].Rc = 0.0; s_pen[wave_id()].fl = 0;
+    s_pen[wave_id()].corrx = 0.0; s_pen[wave_id()].prx = 0.0;
+    s_pen[wave_id()].refx = -__builtin_inf();
+  }
+  if (EXACT && ex) {
+    // the wave's exact sum against its largest value
+    const double Mw = wave_reduce(xs.m, OpMax());
+    double v = xs.s != 0.0 ? xs.s * exp64_neg((xs.m - Mw) * invT, etab) : 0.0;
+    v = wave_reduce(v, OpAdd());
+    if (lane_id() == 0) { w_xs[wave_id()] = v; w_xm[wave_id()] = Mw; }
   }
   const float Rw = wave_reduce(st.R, OpMax());
   double sl = st.s != 0.0 ? __builtin_ldexp(st.s, (int)fmaxf(st.R - Rw, -2048.0f)) : 0.0;
@@ -1365,6 +1437,24 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   }
   const double tol = TOL_S + 2.0 * TOL_T * PR / Ss;
   const bool sum_ok = !anynan && rb_ok && Ss > 0.0 && Ss < __builtin_inf() && tol <= TOL_MAX;
+  // the slice's exact fp64 normaliser against its maximum Ms: the waves' sums
+  // and their penalty corrections, each rescaled to Ms (lane w of each row of
+  // 16 lanes takes wave w).  Kept where the raw terms the corrections
+  // replace are not so large that cancelling them loses the sum's precision.
+  const double Mu = kmx ? (double)key2f(kmx) : -__builtin_inf();
+  const double Ms = Mu > PMX ? Mu : PMX;
+  double Sx = 0.0;
+  bool xok = false;
+  if (EXACT && ex && sum_ok && Ms > -__builtin_inf() && Ms < __builtin_inf()) {
+    const double f = s_pen[lw].refx > -__builtin_inf()
+                         ? exp64_neg((s_pen[lw].refx - Ms) * invT, etab) : 0.0;
+    const double ws = w_xs[lw];
+    const double term = (ws != 0.0 ? ws * exp64_neg((w_xm[lw] - Ms) * invT, etab) : 0.0) +
+                        s_pen[lw].corrx * f;
+    Sx = row0_reduce(term, OpAdd());
+    const double PRx = row0_reduce(s_pen[lw].prx * f, OpAdd());
+    xok = Sx > 0.0 && Sx < __builtin_inf() && PRx < 1e5 * Sx;
+  }
 
   // ---- general: bound the region, write it and the statistics, then finish
   if (wb.n > wb.kw) {
@@ -1403,15 +1493,14 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   }
   __syncthreads();
   if (t == 0) {
-    // the maximum of the slice's penalised values, and the sum against it
-    const double Mu = kmx ? (double)key2f(kmx) : -__builtin_inf();
-    const double Ms = Mu > PMX ? Mu : PMX;
+    // the maximum of the slice's penalised values, and the sums against it
     my->m = Ms;
+    my->sx = xok ? Sx : 0.0;
     my->s = sum_ok ? Ss * exp2(Rb - Ms * kc) : Ss;
     my->tol = tol;
     my->best_v = 0; my->best_i = INT_MAX; my->nan_i = INT_MAX;
     my->tau = Tf; my->ncand = s_cnt;
-    my->flags = (ovf ? SF_OVERFLOW : 0) | (sum_ok ? 0 : SF_INEXACT);
+    my->flags = (ovf ? SF_OVERFLOW : 0) | (sum_ok ? 0 : SF_INEXACT) | (xok ? SF_EXACT : 0);
   }
   // The region finisher runs in slow_kernel, after the grid: a kernel
   // boundary makes the slices' records visible across XCDs without
@@ -1426,27 +1515,29 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   }
 }
 
-template __global__ void sample_kernel<false>(SampleArgs);
-template __global__ void sample_kernel<true>(SampleArgs);
+template __global__ void sample_kernel<false, false>(SampleArgs);
+template __global__ void sample_kernel<true, false>(SampleArgs);
+template __global__ void sample_kernel<false, true>(SampleArgs);
+template __global__ void sample_kernel<true, true>(SampleArgs);
 
 }  // namespace cx
 
 namespace cx {
 int launch_sample(const SampleArgs& A, hipStream_t s) {
-  const void* fn = A.bf16 ? (const void*)sample_kernel<true> : (const void*)sample_kernel<false>;
+  // sliced launches: the kernel that keeps the slices' exact normalisers
+  const int v = (A.bf16 ? 1 : 0) + (A.nsplit > 1 ? 2 : 0);
+  using K = void (*)(SampleArgs);
+  static const K kern[4] = {sample_kernel<false, false>, sample_kernel<true, false>,
+                            sample_kernel<false, true>, sample_kernel<true, true>};
   // Raise the dynamic-LDS limit to what this launch needs (static LDS comes on top).
-  static int attr_set[2] = {0, 0};
-  if (A.lds_bytes > attr_set[A.bf16]) {
-    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, A.lds_bytes);
+  static int attr_set[4] = {0, 0, 0, 0};
+  if (A.lds_bytes > attr_set[v]) {
+    hipError_t e = hipFuncSetAttribute((const void*)kern[v],
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, A.lds_bytes);
     if (e != hipSuccess) return (int)e;
-    attr_set[A.bf16] = A.lds_bytes;
+    attr_set[v] = A.lds_bytes;
   }
-  if (A.bf16)
-    timed_launch(CX_KERNEL_SAMPLE, sample_kernel<true>, dim3(A.B * A.nsplit), dim3(WG),
-                 A.lds_bytes, s, A);
-  else
-    timed_launch(CX_KERNEL_SAMPLE, sample_kernel<false>, dim3(A.B * A.nsplit), dim3(WG),
-                 A.lds_bytes, s, A);
+  timed_launch(CX_KERNEL_SAMPLE, kern[v], dim3(A.B * A.nsplit), dim3(WG), A.lds_bytes, s, A);
   return (int)hipGetLastError();
 }
 }  // namespace cx

@@ -34,7 +34,7 @@ constexpr int PEN_CHUNK = 16384;     // elements per penalties_kernel workgroup
 // normaliser over the row (streamed with its loads ahead when the row has no
 // penalty window), then the region finished with it.  Returns false, with
 // nothing written, if the row still needs the multi-pass path.
-__device__ inline bool refine_row(const SampleArgs& A, int row, unsigned char* dyn, double* red_d,
+__device__ __forceinline__ bool refine_row(const SampleArgs& A, int row, unsigned char* dyn, double* red_d,
                                   int* red_i) {
   const cx_row_params P = A.prm[row];
   SlowRow R;
@@ -54,38 +54,13 @@ __device__ inline bool refine_row(const SampleArgs& A, int row, unsigned char* d
   return finish_row_fast<FIN_CAP>(A, row, P, dyn, red_d, red_i, S) == FIN_DONE;
 }
 
-// Share `part` of `nparts` of a row's exact normaliser: refine_row's sum
-// over the ids of whole 16384-id chunks (part p takes chunks
-// [p n / nparts, (p + 1) n / nparts)).  NaN where refine_row would give up.
-__device__ inline double exact_share(const SampleArgs& A, int row, int part, int nparts,
-                                     unsigned char* dyn, double* red_d) {
-  const cx_row_params P = A.prm[row];
-  SlowRow R;
-  const int wlen = slow_setup(A, row, P, dyn, R);
-  double M = -__builtin_inf();
-  for (int s = 0; s < A.nsplit; ++s) {
-    const double m = A.stats[(size_t)row * A.nsplit + s].m;
-    M = m > M ? m : M;
-  }
-  if (wlen > WIN_MAX || !(M > -__builtin_inf()) || !(M < __builtin_inf()))
-    return __builtin_nan("");
-  const int nch = (A.V + 16383) / 16384;
-  const int lo = (part * nch / nparts) * 16384, hi = ((part + 1) * nch / nparts) * 16384;
-  return R.pen || A.f64 ? exact_norm(R, M, 1.0 / P.temperature, red_d, lo, hi)
-                        : deep_exact_sum(A, row, M, 1.0 / P.temperature, red_d, lo, hi);
-}
-
 __global__ __launch_bounds__(WG) void slow_kernel(SampleArgs A) {
   extern __shared__ __align__(16) unsigned char dyn[];
   __shared__ double red_d[2 * NWAVE + 4];
   __shared__ int red_i[2 * NWAVE + 4];
   __shared__ int s_state;
-  __shared__ double s_sx;
   enum { DECIDED, MULTIPASS, REFINE, FINISH };
-  // with par_exact, nsplit workgroups per row (all but part 0 only share
-  // the exact normaliser of a sliced top-p row)
-  const int nparts = A.par_exact ? A.nsplit : 1;
-  const int row = (int)blockIdx.x / nparts, part = (int)blockIdx.x % nparts;
+  const int row = (int)blockIdx.x;
   if (threadIdx.x == 0) {
     // a sliced row's status word is not written by the fused kernel
     const int st = A.row_status[row];
@@ -98,43 +73,9 @@ __global__ __launch_bounds__(WG) void slow_kernel(SampleArgs A) {
   __syncthreads();
   int state = s_state;
   if (state == DECIDED) return;
-  double S_exact = 0.0;                  // 0: the finisher takes the streamed sums
-  if (nparts > 1) {
-    const cx_row_params& P = A.prm[row];
-    if (state != FINISH || !(P.temperature > 0.0) || !(P.top_p < 1.0) || P.typical_p < 1.0) {
-      if (part != 0) return;
-    } else {
-      // every part sums its share; the last to finish adds the shares in
-      // part order (the count's add releases the share's store; the last
-      // part's acquire fence orders the count before its loads) and takes
-      // the row.  (Two full device fences around a plain add: 1.6 us more
-      // per call at B=64, V=128256.)
-      const double sx = exact_share(A, row, part, nparts, dyn, red_d);
-      if (threadIdx.x == 0) {
-        SplitStats* st = A.stats + (size_t)row * nparts;
-        st[part].xshare = sx;
-        const int done = __hip_atomic_fetch_add(A.counters + row, 1, __ATOMIC_RELEASE,
-                                                __HIP_MEMORY_SCOPE_AGENT) + 1;
-        double S = -1.0;
-        if (done == nparts) {
-          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-          S = 0.0;
-          for (int p = 0; p < nparts; ++p) S += ((volatile SplitStats*)st)[p].xshare;
-          A.counters[row] = 0;             // zero between calls
-          // a NaN or empty sum (where refine_row gives up): the finisher
-          // takes the streamed sums, as without the shares
-          if (!(S > 0.0) || !(S < __builtin_inf())) S = 0.0;
-        }
-        s_sx = S;
-      }
-      __syncthreads();                   // (also: the penalty tables in dyn are dead)
-      S_exact = s_sx;
-      if (S_exact == -1.0) return;
-    }
-  }
   if (state == FINISH) {
     const cx_row_params P = A.prm[row];
-    const int r = finish_row_fast<FIN_CAP>(A, row, P, dyn, red_d, red_i, S_exact);
+    const int r = finish_row_fast<FIN_CAP>(A, row, P, dyn, red_d, red_i);
     if (r == FIN_DONE) return;
     state = r == FIN_REFINE ? REFINE : MULTIPASS;
     __syncthreads();
@@ -283,7 +224,6 @@ int launch_slow(const SampleArgs& A, hipStream_t s) {
   if (int e = set_lds(slow_kernel, bytes, attr)) return e;
   SampleArgs A1 = A;
   A1.pending_only = 0;
-  A1.par_exact = 0;
   if (A.bf16 && !A.all_slow && !A.out_probs) {
     // rows of a bf16 call may take the counted deep-nucleus path:
     // finish16_kernel, then slow_kernel for the rows it hands back
@@ -291,14 +231,8 @@ int launch_slow(const SampleArgs& A, hipStream_t s) {
     timed_launch(CX_KERNEL_SAMPLE_SLOW, finish16_kernel, dim3(A.B), dim3(WG), FIN_CAP * 32, s,
                  A1);
     A1.pending_only = 1;
-  } else if (A.nsplit > 1 && !A.all_slow) {
-    // sliced rows (a small batch: about one workgroup per CU) share the
-    // exact normaliser of their top-p rows over the row's slices' worth of
-    // workgroups, then the last of them finishes the row with it
-    A1.par_exact = 1;
   }
-  timed_launch(CX_KERNEL_SAMPLE_SLOW, slow_kernel, dim3(A.B * (A1.par_exact ? A.nsplit : 1)),
-               dim3(WG), bytes, s, A1);
+  timed_launch(CX_KERNEL_SAMPLE_SLOW, slow_kernel, dim3(A.B), dim3(WG), bytes, s, A1);
   return (int)hipGetLastError();
 }
 
