@@ -19,6 +19,24 @@ FLAGS = [
 ]
 
 
+def build_hist(verbose: bool = False) -> str:
+    """The CPython extension that writes a batch's penalty windows from Python
+    lists (csrc/cx_hist.c), compiled with the host C compiler."""
+    import sysconfig
+    out = os.path.join(HERE, "_cxhist" + sysconfig.get_config_var("EXT_SUFFIX"))
+    cmd = [os.environ.get("CC", "gcc"), "-O2", "-shared", "-fPIC", "-Wall",
+           "-I", sysconfig.get_paths()["include"], "-o", out + ".tmp",
+           os.path.join(CSRC, "cx_hist.c")]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        sys.stderr.write(r.stdout + r.stderr)
+        raise RuntimeError("gcc failed building _cxhist")
+    os.replace(out + ".tmp", out)
+    return out
+
+
 def build(verbose: bool = False) -> str:
     hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
     cmd = [hipcc, *FLAGS, "-I", os.path.join(ROOT, "include"), "-I", CSRC, "-o", LIB + ".tmp",
@@ -30,6 +48,7 @@ def build(verbose: bool = False) -> str:
         sys.stderr.write(r.stdout + r.stderr)
         raise RuntimeError("hipcc failed building libcx_sampler.so")
     os.replace(LIB + ".tmp", LIB)
+    build_hist(verbose)
     return LIB
 
 

@@ -4,8 +4,10 @@
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
+#include <algorithm>
 #include <mutex>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "cx_sampler.h"
@@ -276,8 +278,19 @@ static int verify_impl(const float* target, const float* draft, const int32_t* i
 // Small calls (a decode step's rows) stage their inputs and outputs through a
 // pinned host mirror of the device part: the inputs are packed there with
 // memcpy and cross in one copy, the outputs come back in one copy.  Larger
-// calls copy from and to the caller's memory directly.
+// calls stage their small inputs the same way and send the logits through a
+// ring of pinned chunks (below).
 constexpr size_t STAGE_MAX = (size_t)8 << 20;
+
+// Logits too large for the mirror cross through a ring of pinned chunks:
+// each of up to RING_THREADS host threads fills its own pair of chunks in
+// turn (memcpy from the caller's pageable memory) and queues each chunk's
+// copy on the arena's stream, so the host copies run in parallel with each
+// other and with the DMA engine.  A copy straight from pageable memory goes
+// through the runtime's own bounce buffer one piece at a time, at a fraction
+// of the link's rate.
+constexpr size_t RING_CHUNK = (size_t)4 << 20;
+constexpr int RING_THREADS = 8;
 
 struct Arena {
   int dev = -1;
@@ -289,6 +302,8 @@ struct Arena {
   void* ws = nullptr;
   size_t ws_cap = 0;
   bool ws_dirty = false;
+  char* ring = nullptr;        // 2 * RING_THREADS pinned chunks of RING_CHUNK bytes
+  hipEvent_t ring_ev[2 * RING_THREADS] = {};   // each chunk's last queued copy
 };
 
 static std::mutex g_arena_mu;
@@ -373,6 +388,57 @@ class ArenaLease {
   hipStream_t stream() const { return a_->stream; }
   // the call completed: no refill before the next call
   void finish() { a_->ws_dirty = false; }
+
+  // Queue the copy of n bytes of host memory to device memory on the
+  // arena's stream: through the pinned ring when n spans several chunks,
+  // else directly.  Returns once every chunk's copy is queued (the last ones
+  // may still be in flight; the host buffer is no longer read).
+  int h2d_in(void* dst, const void* src, size_t n) {
+    hipError_t e;
+    if (n <= RING_CHUNK) {
+      if ((e = hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, a_->stream)))
+        return hip_fail(e, "hipMemcpyAsync");
+      return CX_OK;
+    }
+    if (!a_->ring) {
+      if ((e = hipHostMalloc((void**)&a_->ring, 2 * RING_THREADS * RING_CHUNK,
+                             hipHostMallocDefault)) != hipSuccess) {
+        a_->ring = nullptr;
+        return hip_fail(e, "hipHostMalloc(ring)");
+      }
+      for (int i = 0; i < 2 * RING_THREADS; ++i)
+        if ((e = hipEventCreateWithFlags(&a_->ring_ev[i], hipEventDisableTiming)) != hipSuccess)
+          return hip_fail(e, "hipEventCreateWithFlags");
+    }
+    const size_t nch = (n + RING_CHUNK - 1) / RING_CHUNK;
+    const unsigned hc = std::thread::hardware_concurrency();
+    const int T = (int)std::min<size_t>(std::min<size_t>(RING_THREADS, nch), hc ? hc : 1);
+    std::vector<hipError_t> err(T, hipSuccess);
+    auto fill = [&](int t) {
+      hipError_t x = hipSetDevice(a_->dev);
+      for (size_t j = t, i = 0; x == hipSuccess && j < nch; j += T, ++i) {
+        const int b = 2 * t + (int)(i & 1);
+        // the chunk's previous copy (of this call, or of an earlier call
+        // that failed before its stream was drained) has completed
+        if ((x = hipEventSynchronize(a_->ring_ev[b])) != hipSuccess) break;
+        const size_t off = j * RING_CHUNK, len = std::min(RING_CHUNK, n - off);
+        char* buf = a_->ring + (size_t)b * RING_CHUNK;
+        memcpy(buf, (const char*)src + off, len);
+        if ((x = hipMemcpyAsync((char*)dst + off, buf, len, hipMemcpyHostToDevice,
+                                a_->stream)) != hipSuccess)
+          break;
+        x = hipEventRecord(a_->ring_ev[b], a_->stream);
+      }
+      err[t] = x;
+    };
+    std::vector<std::thread> th;
+    for (int t = 1; t < T; ++t) th.emplace_back(fill, t);
+    fill(0);
+    for (auto& x : th) x.join();
+    for (int t = 0; t < T; ++t)
+      if (err[t] != hipSuccess) return hip_fail(err[t], "pinned ring copy");
+    return CX_OK;
+  }
 
  private:
   Arena* a_ = nullptr;
@@ -489,37 +555,44 @@ int cx_sample_host(const void* logits, int32_t dtype, int64_t ld, int32_t B, int
   const size_t nl = (size_t)B * ld * esz, np = sizeof(cx_row_params) * B, nu = 8 * (size_t)B,
                nb = 4 * (size_t)B, nh = ldh > 0 ? (size_t)B * ldh * 4 : 0,
                nhl = ldh > 0 ? nb : 0, npr = out_probs ? (size_t)B * V * 4 : 0;
-  // device pieces: the inputs, then ids and status (staged), then probs
-  const size_t in_bytes = AL::piece(nl) + AL::piece(np) + AL::piece(nu) + AL::piece(nh) +
-                          AL::piece(nhl);
+  // device pieces: the small inputs (and the logits when they fit the
+  // mirror), then ids and status (staged together), then the logits that go
+  // through the pinned ring, then probs
+  const size_t small_in = AL::piece(np) + AL::piece(nu) + AL::piece(nh) + AL::piece(nhl);
+  const bool ring = small_in + AL::piece(nl) + 2 * AL::piece(nb) > STAGE_MAX;
+  const size_t in_bytes = small_in + (ring ? 0 : AL::piece(nl));
   const size_t staged = in_bytes + 2 * AL::piece(nb);
   const bool stage = staged <= STAGE_MAX;
   ArenaLease L;
-  if (int rc = L.acquire(staged + AL::piece(npr), cx_sample_workspace_bytes(B, V, ldh),
-                         stage ? staged : 0))
+  if (int rc = L.acquire(staged + (ring ? AL::piece(nl) : 0) + AL::piece(npr),
+                         cx_sample_workspace_bytes(B, V, ldh), stage ? staged : 0))
     return rc;
-  char* dl = L.take(nl);
   char* dp = L.take(np);
   char* du = L.take(nu);
   char* dh = L.take(nh);
   char* dhl = L.take(nhl);
+  char* dl = ring ? nullptr : L.take(nl);
   char* did = L.take(nb);
   char* dst = L.take(nb);
+  if (ring) dl = L.take(nl);
   char* dpr = out_probs ? L.take(npr) : nullptr;
   const hipStream_t s = L.stream();
   hipError_t e;
   if (stage) {
-    memcpy(L.host(dl), logits, nl);
     memcpy(L.host(dp), prm, np);
     memcpy(L.host(du), u, nu);
     if (ldh > 0) {
       memcpy(L.host(dh), hist, nh);
       memcpy(L.host(dhl), hist_len, nhl);
     }
-    if ((e = h2d(dl, L.host(dl), in_bytes, s))) return hip_fail(e, "hipMemcpyAsync");
-  } else if ((e = h2d(dl, logits, nl, s)) || (e = h2d(dp, prm, np, s)) || (e = h2d(du, u, nu, s)) ||
+    if (!ring) memcpy(L.host(dl), logits, nl);
+    if ((e = h2d(dp, L.host(dp), in_bytes, s))) return hip_fail(e, "hipMemcpyAsync");
+  } else if ((e = h2d(dp, prm, np, s)) || (e = h2d(du, u, nu, s)) ||
              (ldh > 0 && ((e = h2d(dh, hist, nh, s)) || (e = h2d(dhl, hist_len, nhl, s))))) {
     return hip_fail(e, "hipMemcpyAsync");
+  }
+  if (ring) {
+    if (int rc = L.h2d_in(dl, logits, nl)) return rc;
   }
   int rc = sample_impl(dl, dtype, ld, B, V, ldh > 0 ? (const int32_t*)dh : nullptr,
                        ldh > 0 ? (const int32_t*)dhl : nullptr, ldh, (const cx_row_params*)dp,
@@ -583,9 +656,10 @@ static int rowop_host(bool trunc, const void* x, int32_t dtype, int64_t ld, int3
   char* dhl = ldh > 0 ? L.take(nhl) : nullptr;
   const hipStream_t s = L.stream();
   hipError_t e;
-  if ((e = h2d(dx, x, nx, s)) || (e = h2d(dp, prm, np, s)) ||
+  if ((e = h2d(dp, prm, np, s)) ||
       (ldh > 0 && ((e = h2d(dh, hist, nh, s)) || (e = h2d(dhl, hist_len, nhl, s)))))
     return hip_fail(e, "hipMemcpyAsync");
+  if (int rc = L.h2d_in(dx, x, nx)) return rc;
   int rc = rowop_impl(trunc, dx, dtype, ld, B, V, (const int32_t*)dh, (const int32_t*)dhl, ldh,
                       (const cx_row_params*)dp, (double*)dout, V, (int32_t*)dst, s);
   if (rc != CX_OK) return rc;
@@ -654,10 +728,13 @@ int cx_spec_verify_host(const float* target, const float* draft, const int32_t* 
   char* dst = L.take(nb);
   const hipStream_t s = L.stream();
   hipError_t e;
-  if ((e = h2d(dt, target, nt, s)) || (e = h2d(di, draft_ids, ni, s)) ||
-      (e = h2d(du, u, nu, s)) || (e = h2d(dT, temperature, nb, s)) ||
-      (any_stoch && (e = h2d(dd, draft, nd, s))))
+  if ((e = h2d(di, draft_ids, ni, s)) || (e = h2d(du, u, nu, s)) ||
+      (e = h2d(dT, temperature, nb, s)))
     return hip_fail(e, "hipMemcpyAsync");
+  if (int rc = L.h2d_in(dt, target, nt)) return rc;
+  if (any_stoch) {
+    if (int rc = L.h2d_in(dd, draft, nd)) return rc;
+  }
   int rc = verify_impl((const float*)dt, (const float*)dd, (const int32_t*)di,
                        (const double*)du, (const float*)dT, B, gamma, V, (int32_t*)da,
                        (int32_t*)dn, (int32_t*)dus, (int32_t*)dst, L.ws(), L.ws_cap(), s,

@@ -25,12 +25,18 @@ draw, so the generator advances exactly as the reference's does.
 """
 from __future__ import annotations
 
+import array
 import threading
 from typing import Sequence
 
 import numpy as np
 
 from . import _lib
+
+try:
+    from . import _cxhist
+except ImportError as e:          # built beside libcx_sampler.so by build.py
+    raise ImportError("chenxing_amd._cxhist is not built: run chenxing_amd/build.py") from e
 from .params import RowParams, SamplingParams, pack_rows
 
 __all__ = ["Sampler", "SamplingParams"]
@@ -74,21 +80,36 @@ class Sampler:
         return np.random.default_rng(seed)
 
     # ------------------------------------------------------------ arguments
+    @staticmethod
+    def _window_seq(params, generated_ids):
+        """The slice of the history the penalties read (sampler.py:66-67), or
+        None when no penalty is on."""
+        rp = float(params.repetition_penalty)
+        pres = float(getattr(params, "presence_penalty", 0.0))
+        freq = float(getattr(params, "frequency_penalty", 0.0))
+        if rp == 1.0 and pres == 0.0 and freq == 0.0:
+            return None
+        if generated_ids is None or len(generated_ids) == 0:
+            return None
+        n_keep = int(getattr(params, "n_keep", 0))
+        return generated_ids[-max(64, n_keep):] if n_keep else generated_ids
+
     def _window(self, params, generated_ids, V: int):
         """The history handed to the device for one row: the reference's
         penalty window (sampler.py:67) with ids outside [0, vocab_size)
         replaced by -1 (:68).  None when no penalty is on."""
-        rp = float(params.repetition_penalty)
-        pres = float(getattr(params, "presence_penalty", 0.0))
-        freq = float(getattr(params, "frequency_penalty", 0.0))
-        if not generated_ids or (rp == 1.0 and pres == 0.0 and freq == 0.0):
+        seq = self._window_seq(params, generated_ids)
+        if seq is None:
             return None
-        n_keep = int(getattr(params, "n_keep", 0))
-        seq = generated_ids[-max(64, n_keep):] if n_keep else generated_ids
+        rp = float(params.repetition_penalty)
+        freq = float(getattr(params, "frequency_penalty", 0.0))
         if isinstance(seq, np.ndarray):
             h = seq.astype(np.int64)
         else:
             try:
+                # array('q') unboxes a list of ints fastest
+                h = np.frombuffer(array.array("q", seq), dtype=np.int64)
+            except TypeError:
                 h = np.fromiter(seq, dtype=np.int64, count=len(seq))
             except OverflowError:
                 h = np.asarray([t if -1 <= t < 2**62 else -1 for t in seq], dtype=np.int64)
@@ -123,6 +144,47 @@ class Sampler:
             n += c
         groups.append(np.repeat(ids[start:], cnt[start:]).astype(np.int32))
         return groups
+
+    def _windows(self, plist, hists, V: int):
+        """Every row's penalty window: (wins, lists).  Plain lists (or tuples)
+        of at most WINDOW_MAX ids are kept as they are, their rows listed in
+        ``lists``, for _cxhist's C loop; every other window (numpy arrays,
+        long windows, rows indexed beyond a short V) goes through _window."""
+        fast = V >= self.vocab_size
+        wins, lists = [], []
+        for b, (p, h) in enumerate(zip(plist, hists)):
+            seq = self._window_seq(p, h) if fast else None
+            if fast and type(seq) in (list, tuple) and len(seq) <= WINDOW_MAX:
+                wins.append(seq)
+                lists.append(b)
+            else:
+                wins.append(self._window(p, [] if h is None else h, V))
+        return wins, lists
+
+    def _history_arrays(self, wins, lists, plist, hists, V: int):
+        """The int32 [B, H] history and hist_len [B] the library takes (None,
+        None when no row has a window).  Rows of ``lists`` are written by
+        _cxhist.fill; a row it returns (an item that is not a plain int) gets
+        numpy's conversion and errors through _window, as in ``sample``."""
+        on_list = set(lists)
+        H = max((len(w) if b in on_list else w.size for b, w in enumerate(wins)
+                 if w is not None), default=0)
+        if H == 0:
+            return None, None
+        B = len(wins)
+        hist = np.full((B, H), -1, np.int32)
+        hist_len = np.zeros(B, np.int32)
+        if lists:
+            for b in _cxhist.fill([wins[b] for b in lists], lists, hist, hist_len,
+                                  self.vocab_size):
+                wins[b] = self._window(plist[b], hists[b], V)
+                on_list.discard(b)
+                hist[b] = -1
+        for b, w in enumerate(wins):
+            if w is not None and b not in on_list:
+                hist[b, :w.size] = w
+                hist_len[b] = w.size
+        return hist, hist_len
 
     @staticmethod
     def _penalise_groups(row, bf16: bool, params, groups: _Groups) -> np.ndarray:
@@ -211,7 +273,7 @@ class Sampler:
             raise ValueError("need one history per row")
         if B == 0:
             return []
-        wins = [self._window(p, h or [], V) for p, h in zip(plist, hists)]
+        wins, lists = self._windows(plist, hists, V)
         # rows whose window one launch cannot hold: their penalised fp64 rows
         # (group by group), sampled with the penalties off on the exact fp64
         # path; the other rows take the batch launch
@@ -234,15 +296,7 @@ class Sampler:
             for f in ("presence_penalty", "frequency_penalty"):
                 prm_long[f] = 0.0
             prm_long["repetition_penalty"] = 1.0
-        H = max((w.size for w in wins if w is not None), default=0)
-        hist = hist_len = None
-        if H > 0:
-            hist = np.full((B, H), -1, np.int32)
-            hist_len = np.zeros(B, np.int32)
-            for b, w in enumerate(wins):
-                if w is not None:
-                    hist[b, :w.size] = w
-                    hist_len[b] = w.size
+        hist, hist_len = self._history_arrays(wins, lists, plist, hists, V)
         prm = pack_rows(plist)
         stoch = [float(p.temperature) != 0.0 for p in plist]
         seeds = [getattr(p, "seed", None) for p in plist]

@@ -101,3 +101,57 @@ def test_batch_argument_checks():
     with pytest.raises(ValueError):
         s.sample_batch(np.zeros((2, 8), np.float32), [SamplingParams()] * 3)
     assert s.sample_batch(np.zeros((0, 8), np.float32), []) == []
+
+
+def test_batch_history_arrays_equal_the_per_row_windows():
+    """sample_batch writes plain-int lists through _cxhist's C loop and
+    every other window through _window: the arrays must equal the per-row
+    windows, whatever the item types (numpy ints, floats, ints beyond 64
+    bits fall back), ranges, n_keep and penalty settings."""
+    V = 1000
+    s = Sampler(V)
+    rng = np.random.default_rng(5)
+    plist, hists = [], []
+    for b in range(40):
+        n = int(rng.integers(0, 300))
+        ids = [int(t) for t in rng.integers(-5, V + 50, n)]
+        kind = b % 8
+        if kind == 1:
+            ids = tuple(ids)
+        elif kind == 2:
+            ids = np.asarray(ids, dtype=np.int64)
+        elif kind == 3 and ids:
+            ids[len(ids) // 2] = np.int64(ids[len(ids) // 2])   # not an exact int
+        elif kind == 4 and ids:
+            ids[0] = 2 ** 70                                    # beyond 64 bits
+        elif kind == 5:
+            ids = ids + [2 ** 40, -(2 ** 40), 2 ** 31, V - 1, V, 0]
+        pen = [dict(repetition_penalty=1.1), dict(presence_penalty=0.5),
+               dict(frequency_penalty=0.3), dict()][b % 4]
+        plist.append(SamplingParams(n_keep=[0, 70, 3][b % 3], **pen))
+        hists.append(ids)
+    wins, lists = s._windows(plist, hists, V)
+    assert lists                                                # the C loop takes rows
+    hist, hl = s._history_arrays(wins, lists, plist, hists, V)
+    for b in range(40):
+        w = s._window(plist[b], hists[b], V)
+        if w is None:
+            assert hl[b] == 0 and np.all(hist[b] == -1)
+        else:
+            assert hl[b] == w.size
+            assert hist[b, :w.size].tolist() == w.tolist()
+            assert np.all(hist[b, w.size:] == -1)
+
+
+def test_cxhist_fill_edge_cases():
+    from chenxing_amd import _cxhist
+    h = np.full((4, 3), -7, np.int32)
+    hl = np.zeros(4, np.int32)
+    left = _cxhist.fill([[1, 2, 99], [1.0], [1, 2, 3, 4], (5, 2 ** 70)], [0, 1, 2, 3], h, hl, 50)
+    assert left == [1, 2, 3]                     # a float, a row longer than H, 2**70
+    assert h[0].tolist() == [1, 2, -1] and hl[0] == 3
+    assert hl[1:].tolist() == [0, 0, 0]
+    with pytest.raises(IndexError):
+        _cxhist.fill([[1]], [4], h, hl, 50)
+    with pytest.raises(ValueError):
+        _cxhist.fill([[1]], [0], h.astype(np.int64), hl, 50)
