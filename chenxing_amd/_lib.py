@@ -49,6 +49,9 @@ _SIGS = {
     "cx_spec_verify_workspace_bytes": (C.c_size_t, [C.c_int32, C.c_int32, C.c_int32]),
     "cx_spec_verify_host": (C.c_int, [_P, _P, _P, _P, _P, C.c_int32, C.c_int32, C.c_int32, _P,
                                       _P, _P, _P]),
+    "cx_lmhead_argmax_bf16": (C.c_int, [_P, C.c_int64, _P, C.c_int64, C.c_int32, C.c_int32,
+                                        C.c_int32, _P, _P, _P, _P, C.c_size_t, _P]),
+    "cx_lmhead_workspace_bytes": (C.c_size_t, [C.c_int32, C.c_int32]),
     "cx_timing_enable": (C.c_int, [C.c_int]),
     "cx_timing_read": (C.c_int, [C.c_int32, _P, _P]),
     "cx_last_error": (C.c_char_p, []),
@@ -230,6 +233,7 @@ class Workspace:
 
 _ws_sample = Workspace()
 _ws_verify = Workspace()
+_ws_head = Workspace()
 
 
 def _stream_ptr(device):
@@ -319,6 +323,42 @@ def spec_verify_device(target, draft, draft_ids, u, temperature, accepted=None, 
         _P(draft_ids.data_ptr()), _P(u.data_ptr()), _P(temperature.data_ptr()), B, g, V,
         *[_P(o.data_ptr()) for o in outs], _P(ws.data_ptr()), ws.numel(), sp))
     return tuple(outs)
+
+
+def lmhead_argmax_device(hidden, weight, out_id=None, out_max=None, out_logits=None):
+    """LM-head projection with the greedy argmax fused, on the current stream.
+
+    hidden: [B, D] torch.bfloat16 cuda tensor (the final-normed hidden
+    states); weight: [V, D] torch.bfloat16 (the head weights); D a multiple
+    of 128, unit column stride.  Returns (out_id int32 [B], out_max float32
+    [B]); ``out_logits`` ([B, V] float32) is filled when given (verification
+    only)."""
+    import torch
+    lib = load()
+    for name, t in (("hidden", hidden), ("weight", weight)):
+        if t.dim() != 2 or t.stride(1) != 1 or t.dtype != torch.bfloat16 or not t.is_cuda:
+            raise ValueError(f"{name} must be a bfloat16 cuda matrix with unit column stride")
+    B, D = hidden.shape
+    V = weight.shape[0]
+    if weight.shape[1] != D:
+        raise ValueError("hidden and weight differ in D")
+    dev = hidden.device
+    if out_id is None:
+        out_id = torch.empty(B, dtype=torch.int32, device=dev)
+    if out_max is None:
+        out_max = torch.empty(B, dtype=torch.float32, device=dev)
+    if out_logits is not None and (tuple(out_logits.shape) != (B, V) or
+                                   out_logits.dtype != torch.float32 or
+                                   not out_logits.is_contiguous()):
+        raise ValueError("out_logits must be a contiguous float32 [B, V] tensor")
+    sp = _stream_ptr(dev)
+    ws = _ws_head.get(lib.cx_lmhead_workspace_bytes(B, V), dev, sp.value)
+    _check(lib.cx_lmhead_argmax_bf16(
+        _P(hidden.data_ptr()), hidden.stride(0), _P(weight.data_ptr()), weight.stride(0),
+        B, D, V, _P(out_id.data_ptr()), _P(out_max.data_ptr()),
+        _P(out_logits.data_ptr()) if out_logits is not None else None,
+        _P(ws.data_ptr()), ws.numel(), sp))
+    return out_id, out_max
 
 
 def header_symbols() -> list[str]:

@@ -9,7 +9,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libcx_sampler.so")
-SOURCES = ["cx_api.hip", "cx_sample.hip", "cx_slow.hip", "cx_verify.hip"]
+SOURCES = ["cx_api.hip", "cx_sample.hip", "cx_slow.hip", "cx_verify.hip", "cx_head.hip"]
 
 FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",

@@ -39,6 +39,16 @@ static int fail(int code, const char* fmt, ...) {
   return code;
 }
 
+int api_fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
 static int hip_fail(hipError_t e, const char* what) {
   return fail(CX_EHIP, "%s: %s", what, hipGetErrorString(e));
 }

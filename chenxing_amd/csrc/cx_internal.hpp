@@ -218,4 +218,8 @@ inline SampleWorkspace sample_workspace_layout(int B, int ns) {
   return w;
 }
 
+// Record a failure in the thread-local message cx_last_error() returns and
+// return `code` (cx_api.hip); for entry points outside cx_api.hip.
+int api_fail(int code, const char* fmt, ...);
+
 }  // namespace cx

@@ -209,6 +209,32 @@ int cx_spec_verify_host(const float* target, const float* draft, const int32_t* 
                         int32_t* accepted, int32_t* next_tok, int32_t* used,
                         int32_t* row_status);
 
+/*
+ * LM-head projection with the greedy draw fused (transformer.py:102-104,
+ * logits = h @ out_w.T, then sampler.py:114-115, argmax of the row, for a
+ * greedy request with no penalty): the [B, V] logits never reach HBM.
+ * bf16 operands, fp32 accumulation on MFMA.
+ *
+ *  hidden     [B, ldh] bf16 bits: the final-normed hidden states
+ *  weight     [V, ldw] bf16 bits: the head weights (out_w, or the tied
+ *             token embedding)
+ *  D          hidden size, a multiple of 128; rows 16-byte aligned
+ *  out_id     [B] int32: the first index of the row maximum, or of the
+ *             first NaN (numpy's argmax)
+ *  out_max    nullable [B] fp32: that logit
+ *  out_logits nullable [B, V] fp32: every logit (verification only; this
+ *             write is what the fusion saves)
+ *  workspace  device scratch of cx_lmhead_workspace_bytes(B, V) bytes; any
+ *             contents.
+ * Device pointers, stream-ordered, no synchronisation, no allocation.
+ */
+int cx_lmhead_argmax_bf16(const uint16_t* hidden, int64_t ldh, const uint16_t* weight,
+                          int64_t ldw, int32_t B, int32_t D, int32_t V, int32_t* out_id,
+                          float* out_max, float* out_logits, void* workspace, size_t ws_bytes,
+                          void* stream);
+
+size_t cx_lmhead_workspace_bytes(int32_t B, int32_t V);
+
 /* Kernel timing (measurement only).  While enabled, every library kernel is
  * dispatched with a start / stop event pair recorded by the dispatch itself
  * (hipExtLaunchKernel): the kernel's execution interval on its stream.
@@ -224,7 +250,9 @@ int cx_spec_verify_host(const float* target, const float* draft, const int32_t* 
                                       finisher runs in CX_KERNEL_SAMPLE_SLOW) */
 #define CX_KERNEL_PENALTIES     5  /* apply_penalties                 */
 #define CX_KERNEL_TRUNCATE      6  /* _truncate                       */
-#define CX_KERNEL_KINDS         7
+#define CX_KERNEL_LMHEAD        7  /* LM head: projection tiles + argmax keys */
+#define CX_KERNEL_LMHEAD_MERGE  8  /* LM head: per-row merge of the keys */
+#define CX_KERNEL_KINDS         9
 int cx_timing_enable(int on);
 int cx_timing_read(int32_t kernel, double* total_ms, int64_t* launches);
 

@@ -16,6 +16,9 @@ the random variates made explicit (the uniforms are arguments instead of
 * :mod:`oracle.speculative_ref` -- ``chenxing/engine/speculative.py:67-69``
   (``_softmax``) and ``:145-171`` (Leviathan accept/reject and the residual
   ``max(0, p - q)`` resample).
+* :mod:`oracle.lmhead_ref` -- ``chenxing/model/transformer.py:102-104``
+  (``x @ out_w.T``) on bf16 operands with exact products, then the greedy
+  argmax of ``sampler.py:114-115``; with the device's accumulation bound.
 * :mod:`oracle.bf16` -- exact bf16 <-> fp32 conversion (round to nearest even).
 
 How each function is pinned (closed forms, the reference's own known-answer
