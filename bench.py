@@ -136,6 +136,35 @@ class DeviceVerify:
         _lib.spec_verify_device(t, draft, self.ids, self.u, self.T, *self.out)
 
 
+# The LM head with the greedy draw fused: a Llama-3-8B-sized head (hidden
+# size 4096, 128256 tokens) at a decode batch of 16 rows, bf16.
+HEAD_B, HEAD_D, HEAD_V = 16, 4096, 128256
+
+
+class DeviceHead:
+    """Random bf16 hidden states and head weights on the GPU (the weights,
+    1 GB, exceed the Infinity Cache: every step streams them from HBM)."""
+
+    def __init__(self, dev, B=HEAD_B, D=HEAD_D, V=HEAD_V):
+        import torch
+        g = torch.Generator(device=dev)
+        g.manual_seed(7)
+        self.w = (torch.randn(V, D, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        self.h = torch.randn(B, D, generator=g, device=dev).to(torch.bfloat16)
+        self.ids = torch.empty(B, dtype=torch.int32, device=dev)
+        self.mx = torch.empty(B, dtype=torch.float32, device=dev)
+
+    def __call__(self):
+        from chenxing_amd import _lib
+        _lib.lmhead_argmax_device(self.h, self.w, self.ids, self.mx)
+
+    def unfused(self):
+        """The same through torch: F.linear (a library GEMM, hipBLASLt) writes
+        the bf16 logits, then torch.argmax reads them."""
+        import torch
+        return torch.argmax(torch.nn.functional.linear(self.h, self.w), dim=1)
+
+
 def time_steps(fn, steps: int, warmup: int, kernel: int):
     """(ms per step over exactly `steps` calls, mean fused-kernel ms)."""
     import torch
@@ -159,7 +188,7 @@ def time_steps(fn, steps: int, warmup: int, kernel: int):
     torch.cuda.synchronize()
     _lib.timing_enable(False)
     kms, n = _lib.timing_read(kernel)
-    for k in range(7):
+    for k in range(_lib.KERNEL_KINDS):
         _lib.timing_read(k)
     return step_ms, kms / max(n, 1)
 
@@ -226,13 +255,17 @@ OTHER = {  # name: (workload factory, kernel whose launches are timed)
     "hetero_bf16": ("hetero_bf16", {}, 0),
     "spec_verify": ("spec_verify", {}, 2),
     "spec_verify_greedy": ("spec_verify", {"greedy": True}, 2),
+    "lmhead_greedy": ("lmhead", {}, 7),
 }
+
 
 
 def time_other(name: str, dev, steps: int, warmup: int) -> dict:
     import torch
     from chenxing_amd import _lib, workloads as W
     fac, kw, kernel = OTHER[name]
+    if name == "lmhead_greedy":
+        return time_head(dev, steps, warmup)
     wk = getattr(W, fac)(**kw)
     if name.startswith("spec"):
         fn = DeviceVerify(wk, dev)
@@ -248,6 +281,41 @@ def time_other(name: str, dev, steps: int, warmup: int) -> dict:
              "main_kernel_ms": round(km, 5)}
     if not name.startswith("spec"):
         entry["slow_path_rows"] = int(np.sum((fn.st.cpu().numpy() & 0x100) != 0))
+    del fn
+    torch.cuda.empty_cache()
+    return entry
+
+
+def time_head(dev, steps: int, warmup: int) -> dict:
+    """The fused LM head + greedy argmax, beside the unfused library path."""
+    import torch
+    from chenxing_amd import _lib
+    fn = DeviceHead(dev)
+    sm, km = time_steps(fn, steps, warmup, _lib.KERNEL_LMHEAD)
+    for _ in range(warmup):
+        fn.unfused()
+    torch.cuda.synchronize()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(steps):
+        fn.unfused()
+    b.record()
+    torch.cuda.synchronize()
+    um = a.elapsed_time(b) / steps
+    nb = HEAD_V * HEAD_D * 2 + HEAD_B * HEAD_D * 2 + HEAD_B * 8
+    ach = nb / (km / 1e3) / 1e9
+    entry = {"rows_per_s": round(HEAD_B / (sm / 1e3), 1), "ms_per_step": round(sm, 5),
+             "algorithmic_bytes": nb, "step_GBps": round(nb / (sm / 1e3) / 1e9, 1),
+             "main_kernel_ms": round(km, 5),
+             "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBPS,
+                          "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBPS, 4),
+                          "mfma_TFLOPs": round(2 * HEAD_B * HEAD_D * HEAD_V / (km / 1e3) / 1e12,
+                                               1)},
+             "unfused_ms_per_step": round(um, 5),
+             "config": {"B": HEAD_B, "D": HEAD_D, "V": HEAD_V, "dtype": "bf16"},
+             "note": "logits = h @ W.T (bf16, fp32 accumulation) with the argmax fused; "
+                     "unfused = torch F.linear writing bf16 logits, then torch.argmax"}
     del fn
     torch.cuda.empty_cache()
     return entry

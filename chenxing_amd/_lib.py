@@ -371,7 +371,9 @@ def header_symbols() -> list[str]:
 
 
 (KERNEL_SAMPLE, KERNEL_SAMPLE_SLOW, KERNEL_VERIFY_STATS, KERNEL_VERIFY_REST,
- KERNEL_SAMPLE_FINISH, KERNEL_PENALTIES, KERNEL_TRUNCATE) = range(7)
+ KERNEL_SAMPLE_FINISH, KERNEL_PENALTIES, KERNEL_TRUNCATE, KERNEL_LMHEAD,
+ KERNEL_LMHEAD_MERGE) = range(9)
+KERNEL_KINDS = 9
 
 
 def timing_enable(on: bool = True) -> None:
