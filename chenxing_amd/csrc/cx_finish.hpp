@@ -193,7 +193,8 @@ __device__ inline void prefix_cut(int E, const int32_t* sidx, BucketOf bucket_of
     const int pos = hb ? __builtin_ctzll(hb) : n - 1;
     // equal keys land in one bucket: the cut key's whole group is here,
     // contiguous and in ascending ids
-    const uint64_t gb = ballot(l < n && r[0].key == lane_read(r[0].key, pos));
+    const uint64_t kpos = lane_read(r[0].key, pos);     // (read by every lane)
+    const uint64_t gb = ballot(l < n && r[0].key == kpos);
     if (l == pos) {
       out.found = 1; out.overflow = 0; out.bucket = bc; out.pos = pos; out.n = n;
       out.cum = cum; out.prev = prv; out.total = total; out.key = r[0].key; out.idx = r[0].idx;

@@ -474,6 +474,10 @@ __device__ __forceinline__ void append_chunk(WaveBuf& wb,
         }
       }
     }
+    // the wave's appends precede the read of their count (one wave's LDS
+    // operations complete in order; the barrier keeps the compiler from
+    // moving the read above them)
+    __builtin_amdgcn_wave_barrier();
     wb.n = lds_load(wb.cnt);
     return;
   }
@@ -1296,6 +1300,9 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   // list, its penalty corrections (with the penalised values at or above
   // its threshold), its sums and state for the combination
   raise_tau(wb, lds_load(wb.shared));
+  // lanes read below the buffer entries other lanes of the wave wrote (in
+  // order on the hardware; the barrier keeps the compiler from hoisting)
+  __builtin_amdgcn_wave_barrier();
   {
     const int n = wb.n;
     for (int e = lane_id(); e < n; e += 64) {

@@ -1,3 +1,4 @@
+#include <mutex>
 // Runs a deep-nucleus row path on the host (deep_row, cx_deep.hpp, or with
 // MODE 16 deep16_row, cx_deep16.hpp), one workgroup at a time, with every
 // buffer an exact-size heap allocation under AddressSanitizer.  Each row's
@@ -9,6 +10,26 @@ thread_local EmuDim threadIdx;
 EmuDim blockIdx;
 emu::Wave* emu::waves;
 std::barrier<>* emu::block_bar;
+thread_local emu::Where* emu::where;
+
+extern "C" void __sanitizer_print_stack_trace();
+void emu::check_sites(int wi) {
+  static const bool on = getenv("EMU_CHECK_SITES") != nullptr;
+  if (!on) return;
+  Wave& w = waves[wi];
+  int bad = -1;
+  for (int l = 1; l < 64 && bad < 0; ++l)
+    if (w.site_line[l] != w.site_line[0] || strcmp(w.site_file[l], w.site_file[0]) != 0) bad = l;
+  if (bad < 0) return;
+  static std::mutex mu;
+  std::lock_guard<std::mutex> g(mu);
+  const int me = emu::lane();
+  if (me != 0 && me != bad) return;
+  fprintf(stderr, "wave %d: lanes at different exchanges; lane %d at %s:%d, called from:\n", wi,
+          me, w.site_file[me], w.site_line[me]);
+  __sanitizer_print_stack_trace();
+  if (me == bad) _exit(4);
+}
 using namespace cx;
 
 template <class T> static T* rd(FILE* f, size_t n) {

@@ -1,3 +1,4 @@
+#include <mutex>
 // Runs the exact multi-pass row path (slow_row, as slow_kernel runs it for
 // fp64 logits: every row) on the host, one workgroup at a time, with every
 // buffer an exact-size heap allocation under AddressSanitizer.
@@ -7,6 +8,26 @@ thread_local EmuDim threadIdx;
 EmuDim blockIdx;
 emu::Wave* emu::waves;
 std::barrier<>* emu::block_bar;
+thread_local emu::Where* emu::where;
+
+extern "C" void __sanitizer_print_stack_trace();
+void emu::check_sites(int wi) {
+  static const bool on = getenv("EMU_CHECK_SITES") != nullptr;
+  if (!on) return;
+  Wave& w = waves[wi];
+  int bad = -1;
+  for (int l = 1; l < 64 && bad < 0; ++l)
+    if (w.site_line[l] != w.site_line[0] || strcmp(w.site_file[l], w.site_file[0]) != 0) bad = l;
+  if (bad < 0) return;
+  static std::mutex mu;
+  std::lock_guard<std::mutex> g(mu);
+  const int me = emu::lane();
+  if (me != 0 && me != bad) return;
+  fprintf(stderr, "wave %d: lanes at different exchanges; lane %d at %s:%d, called from:\n", wi,
+          me, w.site_file[me], w.site_line[me]);
+  __sanitizer_print_stack_trace();
+  if (me == bad) _exit(4);
+}
 using namespace cx;
 
 static int pow2_at_least(long x) { int p = 1; while (p < x) p <<= 1; return p; }
