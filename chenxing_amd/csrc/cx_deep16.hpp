@@ -52,6 +52,8 @@ struct Deep16Shared {
   double gt[NWAVE * NWAVE];                       // [range][wave]: kept mass above v* (pass 2)
   int eq[NWAVE * NWAVE];                          // [range][wave]: occurrences of v* (pass 2)
   uint32_t snap[NWAVE * D16_WW];                  // [range]: the window's counters at its end
+  uint32_t snapk[NWAVE];                          // [range]: the running maximum's key there
+  uint32_t wk[NWAVE];                             // per wave: its running maximum key
   double wm[NWAVE];
   int we[NWAVE];
   double cut[3];                                  // v*'s term; the cut was robust; mass above its block
@@ -77,9 +79,15 @@ __device__ __forceinline__ uint32_t d16_count(const uint32_t* cw, uint32_t key) 
   return d16_half(cw[key >> 1], key);
 }
 
+// The counter word of the first key of the copied window below key k (the
+// window holds keys k - D16_WIN + 1 .. k, from that word on).
+__device__ __forceinline__ uint32_t d16_win0(uint32_t k) {
+  return k >= (uint32_t)(D16_WIN - 1) ? (k - (D16_WIN - 1)) >> 1 : 0u;
+}
+
 template <bool VEC>
 __device__ inline bool deep16_row_impl(const SampleArgs& A, int row, const cx_row_params& P,
-                                       double M, unsigned char* dyn, double* red_d, int* red_i,
+                                       unsigned char* dyn, double* red_d, int* red_i,
                                        Deep16Shared& sh) {
   const int t = threadIdx.x, l = lane_id(), w = wave_id();
   DeepRow R;
@@ -94,16 +102,7 @@ __device__ inline bool deep16_row_impl(const SampleArgs& A, int row, const cx_ro
   const double invT = 1.0 / P.temperature;
   const int L = ((V + NWAVE * R.step - 1) / (NWAVE * R.step)) * R.step;
   const int nsteps = (V + R.step - 1) / R.step;
-  const uint32_t kM = d16_key(__float_as_uint((float)M) >> 16);
-  // the copied window: counter words kw0 .. kM >> 1 (keys kM - D16_WIN + 1 .. kM)
-  const uint32_t kw0 = kM >= (uint32_t)(D16_WIN - 1) ? (kM - (D16_WIN - 1)) >> 1 : 0u;
-  const int nww = (int)((kM >> 1) - kw0 + 1);
   const double* tab = sh.tab;
-  // term of a key: 0 below the span (and for -inf)
-  auto term = [&](uint32_t key) -> double {
-    const double d = (M - (double)d16_val(key)) * invT;
-    return d < (double)DSPAN ? exp64_neg(-d, tab) : 0.0;
-  };
 
   uint32_t* cw = (uint32_t*)dyn;
   for (int i = t; i < D16_WORDS; i += WG) cw[i] = 0u;
@@ -112,9 +111,14 @@ __device__ inline bool deep16_row_impl(const SampleArgs& A, int row, const cx_ro
   load_exp64_tab(sh.tab);                            // its barrier also orders the clears
 
   // ---- pass 1: count every value (-inf, a masked token, in a register:
-  // masks of more than 65535 ids are common); copy the window at each
-  // range's end
+  // masks of more than 65535 ids are common) and find the maximum (the row
+  // is not streamed before); at each range's end copy the D16_WIN values
+  // below the running maximum.  That covers the final window for every
+  // range: the final maximum kM is at least range r's running maximum kr,
+  // so the final window starts no lower than r's copy, and a key above kr
+  // has no occurrence up to range r's end.
   int ninf = 0;
+  uint32_t kmax = 0u;                                // largest key seen: a finite value's or +inf's when any
   deep_stream<VEC>(R, 0, R.step, t, nsteps, [&](int k, const uint32_t (&wd)[DW]) {
     const int e0 = k * R.step + 16 * t;
 #pragma unroll
@@ -123,19 +127,41 @@ __device__ inline bool deep16_row_impl(const SampleArgs& A, int row, const cx_ro
         const uint32_t key = d16_key(deep_code(wd, j));
         if (key == D16_NEG_INF) ++ninf;
         else atomicAdd(cw + (key >> 1), 1u << ((key & 1u) << 4));
+        kmax = key > kmax ? key : kmax;                // (-inf and NaN keys lie below)
       }
     }
     if ((k + 1) * R.step % L == 0 || k + 1 == nsteps) {
+      const uint32_t wmax = wave_reduce(kmax, OpMax());
+      if (l == 0) sh.wk[w] = wmax;
       __syncthreads();
+      uint32_t kr = 0u;
+#pragma unroll
+      for (int i = 0; i < NWAVE; ++i) kr = sh.wk[i] > kr ? sh.wk[i] : kr;
       const int r = (k * R.step) / L;
-      if (t < nww) {
-        const uint32_t v = cw[kw0 + t];
+      const uint32_t w0 = d16_win0(kr);
+      if (t <= (int)((kr >> 1) - w0)) {
+        const uint32_t v = cw[w0 + t];
         for (int rr = r; rr < (k + 1 == nsteps ? NWAVE : r + 1); ++rr) sh.snap[rr * D16_WW + t] = v;
       }
+      if (t == 0)
+        for (int rr = r; rr < (k + 1 == nsteps ? NWAVE : r + 1); ++rr) sh.snapk[rr] = kr;
       __syncthreads();
     }
   });
-  ninf = block_sum(ninf, red_i);
+  ninf = block_sum(ninf, red_i);                     // (its barriers publish snapk)
+  // the row's maximum, recorded for the paths that may take the row after
+  // this one (the fused kernel did not stream a counted row)
+  const uint32_t kM = sh.snapk[NWAVE - 1];
+  const double M = kM > D16_NEG_INF ? (double)d16_val(kM) : -__builtin_inf();
+  if (t < A.nsplit) A.stats[(size_t)row * A.nsplit + t].m = M;
+  if (!(M > -__builtin_inf()) || !(M < __builtin_inf())) return false;
+  // the final copied window: counter words kw0 .. kM >> 1
+  const uint32_t kw0 = d16_win0(kM);
+  // term of a key: 0 below the span (and for -inf)
+  auto term = [&](uint32_t key) -> double {
+    const double d = (M - (double)d16_val(key)) * invT;
+    return d < (double)DSPAN ? exp64_neg(-d, tab) : 0.0;
+  };
 
   // ---- masses of the WG blocks of 64 keys, block b holding keys
   // 65535 - 64 b - l (lane l): descending value in (b, l).  Wave w takes
@@ -305,11 +331,17 @@ __device__ inline bool deep16_row_impl(const SampleArgs& A, int row, const cx_ro
     // ---- per range, from the copies: wave r takes range r (its counts are
     // the differences of consecutive copies), a lane every 64th kept value
     if (w < NWAVE) {
+      // range w's counts: the differences of consecutive copies, each read
+      // in its own window (a key above a copy's running maximum has no
+      // occurrence there yet)
       const uint32_t* cur = sh.snap + w * D16_WW;
       const uint32_t* prv = w > 0 ? cur - D16_WW : nullptr;
+      const uint32_t kc_ = sh.snapk[w], kp_ = w > 0 ? sh.snapk[w - 1] : 0u;
+      const uint32_t wc = d16_win0(kc_), wp = d16_win0(kp_);
       auto cnt = [&](uint32_t key) -> int {
-        const int i = (int)((key >> 1) - kw0);
-        return (int)d16_half(cur[i], key) - (prv ? (int)d16_half(prv[i], key) : 0);
+        const int a = key <= kc_ ? (int)d16_half(cur[(key >> 1) - wc], key) : 0;
+        const int b = prv && key <= kp_ ? (int)d16_half(prv[(key >> 1) - wp], key) : 0;
+        return a - b;
       };
       double m = 0.0;
       for (int i = l; i < ntt; i += 64) m += (double)cnt(kc + 1 + (uint32_t)i) * tt[i];
@@ -505,10 +537,9 @@ __device__ inline bool deep16_row(const SampleArgs& A, int row, unsigned char* d
                                   int* red_i, Deep16Shared& sh) {
   if (!A.bf16) return false;
   const cx_row_params P = A.prm[row];
-  double M = 0.0;
-  if (!deep_eligible(A, row, P, M, true)) return false;   // (top-k rows too)
-  return A.vec_ok ? deep16_row_impl<true>(A, row, P, M, dyn, red_d, red_i, sh)
-                  : deep16_row_impl<false>(A, row, P, M, dyn, red_d, red_i, sh);
+  if (!deep_candidate(A, row, P, true)) return false;     // (top-k rows too)
+  return A.vec_ok ? deep16_row_impl<true>(A, row, P, dyn, red_d, red_i, sh)
+                  : deep16_row_impl<false>(A, row, P, dyn, red_d, red_i, sh);
 }
 
 }  // namespace cx

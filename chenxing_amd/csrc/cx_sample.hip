@@ -1116,8 +1116,31 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
     for (int i = t; i < X.ns; i += WG) X.hword[i] = HW_EMPTY;
   }
   __syncthreads();
-  load_chunk<BF16>(rs, ch0 + NWAVE, qn);
   const cx_row_params& P = sP;
+  // A single-slice bf16 row that may take the counted deep-nucleus path
+  // (finish16_kernel counts its values, finding its maximum as it goes, and
+  // decides it exactly or hands it to the exact path) is not streamed here:
+  // counting reads the row once.  (Its region would be a candidate list its
+  // nucleus usually outgrows, or, for top-k above 256, one whose upkeep
+  // here, ~50 us a row, costs about what counting the row there does.)
+  // Top-k rows up to 64 keep the one-wave finish below, those up to 256 the
+  // region finisher.  (Counting every top-k row above 64 left the counting
+  // kernel three rounds of workgroups deep: 400 instead of 337 us.)  Such a
+  // row has no penalty window, so nothing below is needed for it.
+  const bool count_row = BF16 && single && !greedy && !A.out_probs &&
+                         !(P.top_k > 0 && P.top_k <= 256) && deep_candidate(A, row, P, true);
+  if (count_row) {
+    if (t == 0) {
+      // no maximum yet (NaN): the counting path finds it and records it
+      my->m = __builtin_nan(""); my->s = 0; my->tol = 0; my->best_v = 0;
+      my->best_i = INT_MAX; my->nan_i = INT_MAX; my->tau = 1u; my->ncand = 0; my->flags = 0;
+      A.out_id[row] = -1;
+      A.row_status[row] = ROW_PENDING;
+      A.counters[row] = ROW_PENDING | MARK_DEEP | (P.top_k > 0 && P.top_k < A.V ? MARK_TOPK : 0);
+    }
+    return;
+  }
+  load_chunk<BF16>(rs, ch0 + NWAVE, qn);
   // index the window entries [wstart, wstart + wlen) whose ids fall in the
   // slice: a bitmap bit and a hash word (id << 12 | count) per distinct id,
   // whose slot its first inserter appends to the dense list
@@ -1143,19 +1166,8 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   __syncthreads();
   const int nd = pen_on ? s_nd : 0;
   CX_LDS int* const gctr = to_lds(&s_gctr);
-  // A single-slice bf16 row that may take the counted deep-nucleus path
-  // (finish16_kernel counts its values from its maximum on, and decides it
-  // exactly or hands it to the exact path) needs only its maximum here: the
-  // greedy stream, with no region.  (Its region would be a candidate list
-  // its nucleus usually outgrows, or, for top-k above 256, one whose upkeep
-  // here, ~50 us a row, costs about what counting the row there does.)
-  // Top-k rows up to 64 keep the one-wave finish below, those up to 256 the
-  // region finisher.  (Counting every top-k row above 64 left the counting
-  // kernel three rounds of workgroups deep: 400 instead of 337 us.)
-  const bool count_row = BF16 && single && !greedy && !A.out_probs &&
-                         !(P.top_k > 0 && P.top_k <= 256) && deep_candidate(A, row, P, true);
   // ---------------------------------------------------------------- greedy
-  if (greedy || count_row) {
+  if (greedy) {
     GreedyState gs{-__builtin_inff(), INT_MAX, INT_MAX};
     stream_greedy<BF16>(rowp, rs, q, qn, nv, lo, hi, s0, pen_on, X, to_lds(&s_chunk), gs);
     double bv = gs.bi == INT_MAX ? -__builtin_inf() : (double)gs.bv;
@@ -1176,15 +1188,7 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
     }
     block_argmax(bv, bi, red_d, red_i);
     ni = block_min(ni, red_i, INT_MAX);
-    if (count_row) {
-      if (t == 0) {
-        my->m = bv; my->s = 0; my->tol = 0; my->best_v = bv; my->best_i = bi; my->nan_i = ni;
-        my->tau = 1u; my->ncand = 0; my->flags = 0;
-        A.out_id[row] = -1;
-        A.row_status[row] = ROW_PENDING;
-        A.counters[row] = ROW_PENDING | MARK_DEEP | (P.top_k > 0 && P.top_k < A.V ? MARK_TOPK : 0);
-      }
-    } else if (single) {
+    if (single) {
       const int tok = ni != INT_MAX ? ni : (bi == INT_MAX ? 0 : bi);
       write_row_result(A, row, CX_ROW_GREEDY, tok);
       write_one_hot(A, row, tok);

@@ -56,6 +56,7 @@ int main(int argc, char** argv) {
     int32_t* ids = (int32_t*)malloc(4 * B);
     int32_t* st = (int32_t*)malloc(4 * B);
     SplitStats* stats = (SplitStats*)calloc(B, sizeof(SplitStats));
+    std::vector<double> maxes;
     for (int b = 0; b < B; ++b) {
       double m = -INFINITY;
       for (int i = 0; i < V; ++i) {
@@ -63,7 +64,11 @@ int main(int argc, char** argv) {
                               : (double)((const float*)x)[(size_t)b * V + i];
         if (v > m) m = v;                       // NaN never wins, as in the fused kernel
       }
-      stats[b].m = m;
+      // the counted path finds the maximum itself (the fused kernel leaves
+      // NaN for a row it does not stream) and records it for the paths
+      // after it: check both
+      stats[b].m = counted ? NAN : m;
+      maxes.push_back(m);
     }
     SampleArgs A;
     memset(&A, 0, sizeof A);
@@ -97,6 +102,12 @@ int main(int argc, char** argv) {
       for (auto& h : th) h.join();
       free(dyn);
       if (!decided) { ids[row] = -2; st[row] = -2; }
+      // a counted row's recorded maximum (when it found a finite one)
+      if (counted && std::isfinite(maxes[row]) && stats[row].m != maxes[row]) {
+        fprintf(stderr, "row %d: recorded maximum %g, the row's is %g\n", row, stats[row].m,
+                maxes[row]);
+        return 5;
+      }
     }
     fwrite(ids, 4, B, out);
     fwrite(st, 4, B, out);
