@@ -130,10 +130,11 @@ __device__ inline void prefix_cut(int E, const int32_t* sidx, BucketOf bucket_of
                                   uint64_t* gk, int32_t* gi, int32_t* ga, double* red_d,
                                   int* red_i, PrefixCut& out) {
   __shared__ int pc_n;
+  __shared__ int pc_bc;
   const int t = threadIdx.x;
   unsigned long long* red_u = (unsigned long long*)red_d;
   bm[t] = 0ull;
-  if (t == 0) pc_n = 0;
+  if (t == 0) { pc_n = 0; pc_bc = INT_MAX; }
   __syncthreads();
   for (int j = t; j < E; j += WG)
     if (elig(j)) atomicAdd(&bm[bucket_of(j)], (unsigned long long)(weight(j) * scale));
@@ -155,13 +156,23 @@ __device__ inline void prefix_cut(int E, const int32_t* sidx, BucketOf bucket_of
   const double tgt = relative ? target * total : target;
   const double be = (double)(base + mine) / scale;
   const bool hit = mine != 0ull && (strict ? be > tgt : be >= tgt);
-  const int bc = block_min(hit ? t : INT_MAX, red_i, INT_MAX);
+  // The running weight is monotone, so the first bucket that reaches the
+  // target is the one nonempty bucket whose weight before it does not: the
+  // last nonempty bucket before it ends at that weight.  Its thread claims
+  // it (no block-wide minimum).
+  const double bp = (double)base / scale;
+  const bool before = base != 0ull && (strict ? bp > tgt : bp >= tgt);
+  if (hit && !before) {
+    pc_bc = t;
+    red_u[2 * NWAVE + 1] = base;                     // the weight before the cut bucket
+  }
+  __syncthreads();
+  const int bc = pc_bc;
   if (bc == INT_MAX) {
     if (t == 0) { out.found = 0; out.overflow = 0; out.total = total; }
     __syncthreads();
     return;
   }
-  if (t == bc) red_u[2 * NWAVE + 1] = base;          // the weight before the cut bucket
   // gather the cut bucket
   for (int j0 = 0; j0 < E; j0 += WG) {
     const int j = j0 + t;
@@ -238,8 +249,21 @@ __device__ inline int finish_bucketed(const SampleArgs& A, int row, const cx_row
     kmax = k > kmax ? k : kmax;
     kmin = k < kmin ? k : kmin;
   }
-  kmax = block_max<unsigned long long>(kmax, (unsigned long long*)red_d, 0ull);
-  kmin = block_min<unsigned long long>(kmin, (unsigned long long*)red_d, ~0ull);
+  {
+    // both extremes with one barrier: every thread reads the waves' partials
+    // (scratch of their own, not written again in this call)
+    __shared__ uint64_t s_ext[2 * NWAVE];
+    const uint64_t wx = wave_max(kmax), wn = wave_min(kmin);
+    if (lane_id() == 0) { s_ext[wave_id()] = wx; s_ext[NWAVE + wave_id()] = wn; }
+    __syncthreads();
+    kmax = 0ull;
+    kmin = ~0ull;
+#pragma unroll
+    for (int w = 0; w < NWAVE; ++w) {
+      kmax = s_ext[w] > kmax ? s_ext[w] : kmax;
+      kmin = s_ext[NWAVE + w] < kmin ? s_ext[NWAVE + w] : kmin;
+    }
+  }
   // value buckets: linear in the value, bucket 0 holding the largest
   const double vmax = key2d(kmax), vmin = key2d(kmin);
   double vs = vmax > vmin ? (double)(NBK - 1) / (vmax - vmin) : 0.0;
@@ -284,13 +308,15 @@ __device__ inline int finish_bucketed(const SampleArgs& A, int row, const cx_row
     if (pc.found) {
       const double cm = pc.cum, cp = pc.prev;
       near = fabs(cm - P.top_p) <= tol * cm || (cp > 0.0 && fabs(cp - P.top_p) <= tol * cp);
-      const int bc = pc.bucket, pos = pc.pos, g0 = pc.g0, g1 = pc.g1;
+      const int bc = pc.bucket, pos = pc.pos, g0 = pc.g0, g1 = pc.g1, nb = pc.n;
+      // entries past the cut bucket dropped; the cut bucket's own (gathered
+      // in ga, a disjoint set) kept before the cut value and for its group's
+      // survivors
       for (int j = t; j < E; j += WG)
-        if (kf[j] && vbucket(j) >= bc) kf[j] = 0;
-      __syncthreads();
-      // the cut bucket's entries before the cut value, and its group's survivors
-      if (t < g0 || (t < g1 && spread_keeps(t - g0, pos + 1 - g0, g1 - g0, A.V <= TIE_NET)))
-        kf[ga[t]] = 1;
+        if (kf[j] && vbucket(j) > bc) kf[j] = 0;
+      if (t < nb)
+        kf[ga[t]] = t < g0 || (t < g1 && spread_keeps(t - g0, pos + 1 - g0, g1 - g0,
+                                                      A.V <= TIE_NET));
       __syncthreads();
       complete = true;
     } else {
@@ -313,11 +339,13 @@ __device__ inline int finish_bucketed(const SampleArgs& A, int row, const cx_row
 
   // ---- normalise and draw in token-id order: the first id whose running
   // mass passes u times the kept total (Generator.choice)
+  // (the draw's target is relative to the kept total: Z itself is needed
+  // only for the probabilities written out)
   double z = 0.0;
   int lastk = -1;
   for (int j = t; j < E; j += WG)
     if (kf[j]) { z += sv[j]; lastk = max(lastk, sidx[j]); }
-  const double Z = block_sum(z, red_d);
+  const double Z = A.out_probs ? block_sum(z, red_d) : 0.0;
   prefix_cut(E, sidx, ibucket, ikey, mass, kept, FX_MASS, A.u[row], true, true, bm, gk, gi, ga,
              red_d, red_i, pc);
   if (pc.overflow) return FIN_SORTED;
