@@ -122,37 +122,37 @@ struct PrefixCut {
 // target is a fraction of the total.  Weights are scaled by `scale` into
 // integers (1 for counts).  On return `out` (shared) holds the cut and, with
 // `found`, ga[0 .. n) the region indices of the cut bucket's entries in
-// order.  All threads; uniform result.
+// order.  All threads; uniform result.  The caller hands over bm zeroed and
+// ctr = {0, INT_MAX} (the gather count and the cut bucket), both written
+// before a barrier that precedes the call (one barrier less per cut).
 template <typename BucketOf, typename KeyOf, typename Weight, typename Elig>
 __device__ inline void prefix_cut(int E, const int32_t* sidx, BucketOf bucket_of, KeyOf key_of,
                                   Weight weight, Elig elig, double scale, double target,
-                                  bool relative, bool strict, unsigned long long* bm,
+                                  bool relative, bool strict, unsigned long long* bm, int* ctr,
                                   uint64_t* gk, int32_t* gi, int32_t* ga, double* red_d,
-                                  int* red_i, PrefixCut& out) {
-  __shared__ int pc_n;
-  __shared__ int pc_bc;
+                                  PrefixCut& out) {
+  int& pc_n = ctr[0];
+  int& pc_bc = ctr[1];
   const int t = threadIdx.x;
   unsigned long long* red_u = (unsigned long long*)red_d;
-  bm[t] = 0ull;
-  if (t == 0) { pc_n = 0; pc_bc = INT_MAX; }
-  __syncthreads();
   for (int j = t; j < E; j += WG)
     if (elig(j)) atomicAdd(&bm[bucket_of(j)], (unsigned long long)(weight(j) * scale));
   __syncthreads();
-  // exclusive scan of the buckets (thread t owns bucket t)
+  // exclusive scan of the buckets (thread t owns bucket t): every thread
+  // reads the waves' totals, so the scan across waves costs no barrier
   const unsigned long long mine = bm[t];
   const unsigned long long inc = wave_incl_scan_u64(mine);
   if (lane_id() == 63) red_u[wave_id()] = inc;
   __syncthreads();
-  if (t < 64) {
-    const unsigned long long w = t < NWAVE ? red_u[t] : 0ull;
-    const unsigned long long x = wave_incl_scan_u64(w);
-    if (t < NWAVE) red_u[NWAVE + t] = x - w;
-    if (t == NWAVE - 1) red_u[2 * NWAVE] = x;
+  unsigned long long wbase = 0ull, all = 0ull;
+#pragma unroll
+  for (int w = 0; w < NWAVE; ++w) {
+    const unsigned long long x = red_u[w];
+    wbase += w < wave_id() ? x : 0ull;
+    all += x;
   }
-  __syncthreads();
-  const unsigned long long base = red_u[NWAVE + wave_id()] + (inc - mine);
-  const double total = (double)red_u[2 * NWAVE] / scale;
+  const unsigned long long base = wbase + (inc - mine);
+  const double total = (double)all / scale;
   const double tgt = relative ? target * total : target;
   const double be = (double)(base + mine) / scale;
   const bool hit = mine != 0ull && (strict ? be > tgt : be >= tgt);
@@ -236,11 +236,21 @@ __device__ inline int finish_bucketed(const SampleArgs& A, int row, const cx_row
                                       double invT, double S, double tol, bool exact,
                                       double* red_d, int* red_i) {
   __shared__ PrefixCut pc;
+  __shared__ int s_ctr[6];                           // per cut: gather count, cut bucket
   const int t = threadIdx.x;
-  unsigned long long* bm = (unsigned long long*)sc;
-  uint64_t* gk = (uint64_t*)(sc + NBK);
+  // the gathered bucket, then the buckets of the three cuts (top-k, top-p,
+  // draw), all cleared here, before the barrier below
+  uint64_t* gk = (uint64_t*)sc;
   int32_t* gi = (int32_t*)(gk + GBK);
   int32_t* ga = gi + GBK;
+  unsigned long long* bmk = (unsigned long long*)(sc + 2 * GBK);
+  unsigned long long* bmp = bmk + NBK;
+  unsigned long long* bmd = bmp + NBK;
+  static_assert(2 * GBK + 3 * NBK <= FIN_CAP, "finisher scratch");
+  bmk[t] = 0ull;
+  bmp[t] = 0ull;
+  bmd[t] = 0ull;
+  if (t < 6) s_ctr[t] = (t & 1) ? INT_MAX : 0;
   uint64_t kmax = 0ull, kmin = ~0ull;
   for (int j = t; j < E; j += WG) {
     const uint64_t k = skey[j];
@@ -286,8 +296,8 @@ __device__ inline int finish_bucketed(const SampleArgs& A, int row, const cx_row
   // ---- top-k: every value >= the k-th largest (ties kept)
   if (P.top_k > 0) {
     if (P.top_k <= E) {
-      prefix_cut(E, sidx, vbucket, vkey, one, every, 1.0, (double)P.top_k, false, false, bm, gk,
-                 gi, ga, red_d, red_i, pc);
+      prefix_cut(E, sidx, vbucket, vkey, one, every, 1.0, (double)P.top_k, false, false, bmk,
+                 s_ctr, gk, gi, ga, red_d, pc);
       if (pc.overflow || !pc.found) return FIN_SORTED;
       const uint64_t kth = pc.key;
       for (int j = t; j < E; j += WG) kf[j] = skey[j] >= kth;
@@ -301,8 +311,8 @@ __device__ inline int finish_bucketed(const SampleArgs& A, int row, const cx_row
   // desc, id asc) order whose running mass reaches top_p; of the cut
   // value's group, the survivors spread over its ids
   if (P.top_p < 1.0) {
-    prefix_cut(E, sidx, vbucket, vkey, mass, kept, FX_MASS, P.top_p, false, false, bm, gk, gi, ga,
-               red_d, red_i, pc);
+    prefix_cut(E, sidx, vbucket, vkey, mass, kept, FX_MASS, P.top_p, false, false, bmp, s_ctr + 2,
+               gk, gi, ga, red_d, pc);
     if (pc.overflow) return FIN_SORTED;
     bool near;
     if (pc.found) {
@@ -346,8 +356,8 @@ __device__ inline int finish_bucketed(const SampleArgs& A, int row, const cx_row
   for (int j = t; j < E; j += WG)
     if (kf[j]) { z += sv[j]; lastk = max(lastk, sidx[j]); }
   const double Z = A.out_probs ? block_sum(z, red_d) : 0.0;
-  prefix_cut(E, sidx, ibucket, ikey, mass, kept, FX_MASS, A.u[row], true, true, bm, gk, gi, ga,
-             red_d, red_i, pc);
+  prefix_cut(E, sidx, ibucket, ikey, mass, kept, FX_MASS, A.u[row], true, true, bmd, s_ctr + 4,
+             gk, gi, ga, red_d, pc);
   if (pc.overflow) return FIN_SORTED;
   // u beyond the last step by rounding: the last kept id
   const int tok = pc.found ? pc.idx : block_max(lastk, red_i, -1);
