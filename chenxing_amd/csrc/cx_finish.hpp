@@ -428,17 +428,23 @@ __device__ inline int finish_row_fast(const SampleArgs& A, int row, const cx_row
   if (exact) {
     S = S_exact;
   } else if (flags & SF_EXACT) {
-    // the slices' exact fp64 sums (sliced top-p rows), when every slice has
-    // one: S = sum over slices of sx_s exp((m_s - M) / T)
+    // the slices' fp64 sums (sliced top-p rows), when every slice has one:
+    // S = sum over slices of sx_s exp((m_s - M) / T), exact when every
+    // slice's is, else within the slices' bounds (split sums)
     bool allx = true;
-    double Sx = 0.0;
+    double Sx = 0.0, Bx = 0.0;
     for (int s = 0; s < nsp; ++s) {
       allx = allx && (st[s].flags & SF_EXACT);
-      if ((st[s].flags & SF_EXACT) && st[s].sx != 0.0) Sx += st[s].sx * exp((st[s].m - M) * invT);
+      if ((st[s].flags & SF_EXACT) && st[s].sx != 0.0) {
+        const double v = st[s].sx * exp((st[s].m - M) * invT);
+        Sx += v;
+        Bx += (double)st[s].sxtol * v;
+      }
     }
     if (allx && Sx > 0.0 && Sx < __builtin_inf()) {
       S = Sx;
-      exact = true;
+      if (Bx == 0.0) exact = true;
+      else tol = Bx / Sx * 1.000001 + 1e-15;
     }
   }
   // Degenerate rows (NaN / +inf / all -inf), tie floods, typical-p and a

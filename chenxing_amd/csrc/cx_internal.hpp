@@ -21,7 +21,7 @@ constexpr double TOL_MAX = 1e-4;          // rows whose bound exceeds this are r
 constexpr int SF_OVERFLOW = 1;            // a wave buffer flooded with ties
 constexpr int SF_UNSUPPORTED = 2;         // window longer than WIN_MAX
 constexpr int SF_INEXACT = 4;             // the slice's normaliser has no usable error bound
-constexpr int SF_EXACT = 8;               // sx holds the slice's exact fp64 normaliser
+constexpr int SF_EXACT = 8;               // sx holds the slice's fp64 normaliser (bound sxtol)
 
 
 // Internal row_status values, never returned to the caller, for slow_kernel:
@@ -50,9 +50,10 @@ struct SplitStats {       // one per (row, slice), 64 bytes
   uint32_t tau;           // region threshold key; <= 1 means the region is the whole slice
   int32_t ncand;          // region entries written to the workspace
   int32_t flags;
-  int32_t pad1;
+  float sxtol;            // with SF_EXACT: relative error bound of sx (0: every term
+                          // within 1 ulp; else the split sum's)
   double sx;              // with SF_EXACT: sum of exp((x - m) / T) over the slice in fp64
-                          // (each term within 1 ulp; sliced top-p rows)
+                          // (sliced top-p rows)
 };
 static_assert(sizeof(SplitStats) == 64, "SplitStats layout");
 

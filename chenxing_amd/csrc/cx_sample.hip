@@ -236,6 +236,11 @@ struct WaveBuf {
   float tauf;     // tau as a float; -inf while tau <= 1 (everything)
   int kw;         // entries a compaction keeps
   bool overflow;
+  // split normaliser (see XSum): entries [0, xn) of the buffer are already
+  // in the wave's exact sum; lossy: an insertion took the one-by-one path,
+  // whose compactions the split sum does not follow
+  int xn;
+  bool lossy;
 };
 
 __device__ __forceinline__ void raise_tau(WaveBuf& w, uint32_t t) {
@@ -436,6 +441,57 @@ __device__ __forceinline__ void rescale(float vmax, float c, float lim, SState& 
   }
 }
 
+// An exact fp64 running sum of exp((x - m) / T), each term within 1 ulp
+// (exp64_neg), against a reference m at or above every summed x (the sum is
+// rescaled by exp((m_old - m) / T) when m rises).  Kept only by the
+// sliced-launch kernel, for stochastic top-p rows, so that the row's
+// normaliser needs no second read of the row, in one of two forms:
+//  - full (rows with a penalty window or a top-k): every element of the
+//    lane, against the lane's largest value;
+//  - split (the other top-p rows): only the elements the wave buffer took,
+//    against the wave's largest buffered value.  Each buffered entry is
+//    summed once, from the buffer: before a compaction drops entries, and
+//    at the stream's end for the rest.  The elements below the wave's
+//    threshold when they arrived (SState::t) are summed as the stream sum
+//    is, within TOL_S of their exact total, and that total is a small part
+//    of a top-p row's normaliser: the buffered elements are the row's
+//    largest, which carry the nucleus.  The two add up to the slice's
+//    normaliser within TOL_S times the below-threshold part, and the
+//    fp64 exponentials are taken for a few entries per lane, not for every
+//    element.
+struct XSum {
+  double s, m;
+};
+__device__ __forceinline__ void xsum_raise(XSum& xs, double cm, double invT, const double* etab) {
+  if (cm > xs.m) {
+    if (xs.s != 0.0) xs.s *= exp64_neg((xs.m - cm) * invT, etab);
+    xs.m = cm;
+  }
+}
+// Split form: add the exact terms of wave buffer entries [from, to) (bounds
+// wave-uniform, to <= CAPW), raising the wave-uniform reference to their
+// largest value first.
+__device__ __forceinline__ void xsum_entries(const WaveBuf& wb, int from, int to, double invT,
+                                             const double* etab, XSum& xs) {
+  constexpr int PER = CAPW / 64;
+  // entries other lanes of the wave wrote (in order on the hardware; the
+  // barrier keeps the compiler from hoisting the reads)
+  __builtin_amdgcn_wave_barrier();
+  float v[PER];
+  float vm = -__builtin_inff();
+#pragma unroll
+  for (int e = 0; e < PER; ++e) {
+    const int pos = from + lane_id() + 64 * e;
+    v[e] = pos < to ? key2f(wb.key[pos]) : -__builtin_inff();
+    vm = fmaxf(vm, v[e]);
+  }
+  xsum_raise(xs, (double)wave_reduce(vm, OpMax()), invT, etab);
+  if (!(xs.m > -__builtin_inf())) return;            // nothing buffered yet
+#pragma unroll
+  for (int e = 0; e < PER; ++e)
+    if (v[e] > -__builtin_inff()) xs.s += exp64_neg(((double)v[e] - xs.m) * invT, etab);
+}
+
 // Append the candidates of one chunk (some lane of the wave has one: its
 // chunk maximum reaches the threshold).  Penalised elements never enter:
 // their penalised values join afterwards.
@@ -450,7 +506,9 @@ template <bool BF16>
 __device__ __forceinline__ void append_chunk(WaveBuf& wb,
                                              const float (&xs)[Elem<BF16>::U][Elem<BF16>::NE],
                                              bool flagged, int vb, int nv, int lo, bool pen_on,
-                                             const PenIndex& X, bool share, uint32_t& ck) {
+                                             const PenIndex& X, bool share, uint32_t& ck,
+                                             bool exs, double invT, const double* etab,
+                                             XSum& xsum) {
   using E = Elem<BF16>;
   constexpr int NE = E::NE;
   constexpr int U = E::U;
@@ -508,12 +566,23 @@ __device__ __forceinline__ void append_chunk(WaveBuf& wb,
   int incl = wave_scan_dpp(c);
   int total = __builtin_amdgcn_readlane(incl, 63);
   if (wb.n + total > CAPW && wb.n > wb.kw) {
-    // make room first: keep the kw largest held, raising the threshold
+    // make room first: keep the kw largest held, raising the threshold (the
+    // split sum takes every held entry first, the dropped and the kept)
+    if (exs) xsum_entries(wb, wb.xn, wb.n, invT, etab, xsum);
     wave_compact(wb, share);
-    m = select();
-    c = __popc(m);
-    incl = wave_scan_dpp(c);
-    total = __builtin_amdgcn_readlane(incl, 63);
+    if (exs) wb.xn = wb.n;
+    // The split sum left this chunk's marked slots out of its
+    // below-threshold part: they are written as marked, those under the
+    // raised threshold included (the next compaction drops them, summed).
+    // Where they no longer fit, the raised threshold selects again and the
+    // slots under it are counted nowhere: the slice's split sum is lost.
+    if (!exs || wb.n + total > CAPW) {
+      if (exs) wb.lossy = true;
+      m = select();
+      c = __popc(m);
+      incl = wave_scan_dpp(c);
+      total = __builtin_amdgcn_readlane(incl, 63);
+    }
   }
   if (wb.n + total <= CAPW) {
     // each lane writes its slots at its offset in the wave's prefix sum
@@ -536,6 +605,7 @@ __device__ __forceinline__ void append_chunk(WaveBuf& wb,
     wb.n += total;
     if (lane_id() == 0) *wb.cnt = wb.n;
   } else {
+    if (exs) wb.lossy = true;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const float (&x)[NE] = xs[u];
@@ -558,22 +628,9 @@ __device__ __forceinline__ void append_chunk(WaveBuf& wb,
 // two chunks (wave_id() and wave_id() + NWAVE), loaded by the caller.  The
 // loop alternates between the two buffers (no register copies, which would
 // wait for the chunk still in flight): it consumes one and refills it with
-// the chunk after the other, so two chunks stay in flight.
-// An exact fp64 running sum of exp((x - m) / T) over one lane's elements,
-// against m, the largest value the lane has seen (rescaled by exp((m_old -
-// m) / T) when m rises): each term within 1 ulp (exp64_neg).  Kept only by
-// the sliced-launch kernel, for stochastic top-p rows, so that the row's
-// exact normaliser needs no second read of the row.
-struct XSum {
-  double s, m;
-};
-__device__ __forceinline__ void xsum_raise(XSum& xs, double cm, double invT, const double* etab) {
-  if (cm > xs.m) {
-    if (xs.s != 0.0) xs.s *= exp64_neg((xs.m - cm) * invT, etab);
-    xs.m = cm;
-  }
-}
-
+// the chunk after the other, so two chunks stay in flight.  ex, exs: the
+// slice keeps the full or the split exact fp64 normaliser (XSum); with the
+// split one, st.s sums only the elements below the wave threshold.
 template <bool BF16, bool EXACT>
 __device__ __forceinline__ void stream_stoch(__amdgpu_buffer_rsrc_t rs,
                                              typename Elem<BF16>::V (&q)[Elem<BF16>::U],
@@ -582,7 +639,8 @@ __device__ __forceinline__ void stream_stoch(__amdgpu_buffer_rsrc_t rs,
                                              int krow, int pub_r, CX_LDS int* chunk_ctr,
                                              CX_LDS uint32_t* slots, CX_LDS uint32_t* w_pub,
                                              SState& st, WaveBuf& wb, uint32_t& ck, bool ex,
-                                             double invT, const double* etab, XSum& xs) {
+                                             bool exs, double invT, const double* etab,
+                                             XSum& xs) {
   using E = Elem<BF16>;
   using V = typename E::V;
   constexpr int NE = E::NE;
@@ -600,6 +658,9 @@ __device__ __forceinline__ void stream_stoch(__amdgpu_buffer_rsrc_t rs,
   // consume chunk ch from buffer b, refill b with the chunk after cn
   auto step = [&](V (&b)[U]) {
     raise_tau(wb, lds_load(wb.shared));
+    // the split sum's tail: elements below the threshold this chunk's
+    // appends start from (NaN: every element, the other rows)
+    const float tfs = EXACT && exs ? wb.tauf : __builtin_nanf("");
     const int vb = ch * CH + lane_id();
     float x[U][NE];
 #pragma unroll
@@ -618,7 +679,11 @@ __device__ __forceinline__ void stream_stoch(__amdgpu_buffer_rsrc_t rs,
 #pragma unroll
     for (int u = 0; u < U; ++u)
 #pragma unroll
-      for (int j = 0; j < NE; ++j) ts += __builtin_amdgcn_exp2f(__builtin_fmaf(x[u][j], c, st.nR));
+      for (int j = 0; j < NE; ++j) {
+        const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(x[u][j], c, st.nR));
+        if (EXACT) ts += !(x[u][j] >= tfs) ? e : 0.0f;
+        else ts += e;
+      }
     st.s += (double)ts;
     // The sum is taken here, before the refill below.  Left free, the
     // compiler sinks it past the refill, the refill then needs registers
@@ -639,7 +704,8 @@ __device__ __forceinline__ void stream_stoch(__amdgpu_buffer_rsrc_t rs,
     }
     const bool flagged = cmax >= wb.tauf;
     if (ballot(flagged)) {
-      append_chunk<BF16>(wb, x, flagged, vb, nv, lo, pen_on, X, share, ck);
+      append_chunk<BF16>(wb, x, flagged, vb, nv, lo, pen_on, X, share, ck, EXACT && exs, invT,
+                         etab, xs);
       fresh = true;
     }
     const int cnn = cn < nch ? __builtin_amdgcn_readfirstlane(next_chunk(chunk_ctr)) : nch;
@@ -1203,8 +1269,11 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   const float c = (float)(1.4426950408889634 / P.temperature);
   const double kc = (double)c;
   // the exact fp64 slice normaliser: sliced top-p rows, whose cut the
-  // finisher otherwise could only refine with a second read of the row
-  const bool ex = EXACT && P.top_p < 1.0;
+  // finisher otherwise could only refine with a second read of the row;
+  // split (XSum) for rows with neither a penalty window nor a top-k whose
+  // slice is whole vectors, full for the others
+  const bool exs = EXACT && P.top_p < 1.0 && P.top_k <= 0 && !pen_on && s0 >= hi;
+  const bool ex = EXACT && P.top_p < 1.0 && !exs;
   const double invT = 1.0 / P.temperature;
   const double* etab = EXACT ? (const double*)s_etab : nullptr;
   XSum xs{0.0, -__builtin_inf()};
@@ -1217,6 +1286,8 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   wb.tau = 1u;
   wb.tauf = -__builtin_inff();
   wb.overflow = false;
+  wb.xn = 0;
+  wb.lossy = false;
   // Entries a wave keeps: k for top-k rows; otherwise an equal share of the
   // region finisher's capacity, so the merged region fits in its LDS.
   const int share = max(8, min(KW_MAX, FIN_CAP / (NWAVE * A.nsplit)));
@@ -1292,8 +1363,11 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   CX_LDS uint64_t* const lgk = to_lds(gk);
   CX_LDS int32_t* const lgi = to_lds(gi);
   CX_LDS int* const lcnt = to_lds(&s_cnt);
-  stream_stoch<BF16, EXACT>(rs, q, qn, nv, lo, pen_on, X, c, krow, pub_r, to_lds(&s_chunk),
-                            lslots, lpub, st, wb, ck, ex, invT, etab, xs);
+  {
+    CX_LDS int* const cc = to_lds(&s_chunk);
+    stream_stoch<BF16, EXACT>(rs, q, qn, nv, lo, pen_on, X, c, krow, pub_r, cc, lslots, lpub,
+                              st, wb, ck, ex, exs, invT, etab, xs);
+  }
   if (s0 < hi) {
     raise_tau(wb, lds_load(wb.shared));
     stream_scalar<BF16, EXACT>(rowp, s0, lo, hi, pen_on, X, c, true, st, wb, ck, ex, invT, etab,
@@ -1327,7 +1401,9 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
     s_pen[wave_id()].corrx = 0.0; s_pen[wave_id()].prx = 0.0;
     s_pen[wave_id()].refx = -__builtin_inf();
   }
-  if (EXACT && ex) {
+  // split sum: the entries buffered since the last compaction
+  if (EXACT && exs) xsum_entries(wb, wb.xn, wb.n, invT, etab, xs);
+  if (EXACT && (ex || exs)) {
     // the wave's exact sum against its largest value
     const double Mw = wave_reduce(xs.m, OpMax());
     double v = xs.s != 0.0 ? xs.s * exp64_neg((xs.m - Mw) * invT, etab) : 0.0;
@@ -1348,7 +1424,7 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
     w_R[wave_id()] = Rw;
     w_tau[wave_id()] = wb.tau;
     w_kmx[wave_id()] = kmx_w;
-    w_fl[wave_id()] = fl | (wb.overflow ? 2 : 0);
+    w_fl[wave_id()] = fl | (wb.overflow ? 2 : 0) | (wb.lossy ? 4 : 0);
   }
   __syncthreads();
   const int lw = lane_id() & 15;       // lane w of row 0 reads wave w's record
@@ -1454,7 +1530,7 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   // replace are not so large that cancelling them loses the sum's precision.
   const double Mu = kmx ? (double)key2f(kmx) : -__builtin_inf();
   const double Ms = Mu > PMX ? Mu : PMX;
-  double Sx = 0.0;
+  double Sx = 0.0, xtol = 0.0;
   bool xok = false;
   if (EXACT && ex && sum_ok && Ms > -__builtin_inf() && Ms < __builtin_inf()) {
     const double f = s_pen[lw].refx > -__builtin_inf()
@@ -1466,15 +1542,67 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
     const double PRx = row0_reduce(s_pen[lw].prx * f, OpAdd());
     xok = Sx > 0.0 && Sx < __builtin_inf() && PRx < 1e5 * Sx;
   }
+  if (EXACT && exs && !anynan && rb_ok && !(flw & 4) && Ss < __builtin_inf() &&
+      Ms > -__builtin_inf() && Ms < __builtin_inf()) {
+    // split (Ss holds only the below-threshold terms, and may be 0): the
+    // buffered entries' exact terms plus the below-threshold ones, both
+    // against Ms; the bound is TOL_S of the latter (with a margin for the
+    // fp64 roundings of the sums)
+    const double ws = w_xs[lw];
+    const double Sa = row0_reduce(ws != 0.0 ? ws * exp64_neg((w_xm[lw] - Ms) * invT, etab) : 0.0,
+                                  OpAdd());
+    const double Stm = Ss != 0.0 ? Ss * exp2(Rb - Ms * kc) : 0.0;
+    Sx = Sa + Stm;
+    xok = Sx > 0.0 && Sx < __builtin_inf();
+    xtol = xok ? TOL_S * Stm / Sx + 1e-12 : 0.0;
+  }
 
   // ---- general: bound the region, write it and the statistics, then finish
-  if (wb.n > wb.kw) {
-    wave_compact(wb, false);
-    if (lane_id() == 0) w_tau[wave_id()] = wb.tau;
+  // The region is every buffered entry at or above T, and every element at
+  // or above Tf is buffered.  T is the lowest boundary of a 512-bin
+  // histogram of the buffered keys in [Tf, kmx] with at most NWAVE * kw
+  // entries at or above it (the same bound the waves' own compactions to kw
+  // entries gave, in one pass and one barrier).  The bins are the top-k
+  // finish's rank counters, zeroed at the start and unused on this path.
+  {
+    static_assert(2 * LEAN_CAP == 512, "histogram bins");
+    CX_LDS int* const bins = to_lds(&s_lean.rv[0]);     // rv, then ri: 512 counters
+    const uint32_t lo = Tf > 1u ? Tf : 1u;
+    const uint32_t d = kmx > lo ? kmx - lo : 0u;
+    const int sh = d ? max(0, 23 - (int)__clz(d)) : 0;  // d >> sh < 512
+    const uint32_t base = lo >> sh;
+    __builtin_amdgcn_wave_barrier();
+    for (int e = lane_id(); e < wb.n; e += 64) {
+      const uint32_t k = wb.key[e];
+      if (k >= lo) __hip_atomic_fetch_add(bins + min((int)((k >> sh) - base), 511), 1,
+                                          CX_RELAXED_WG);
+    }
+    if (t == 0) s_cnt = 0;
+    __syncthreads();
+    // every wave: lane l holds bins 8l .. 8l + 7; the lowest bin b whose
+    // suffix count is at most the cap
+    const int cap = NWAVE * wb.kw;
+    int cb[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) cb[j] = lds_load(bins + 8 * lane_id() + j);
+    int lsum = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) lsum += cb[j];
+    const int incl = wave_scan_dpp(lsum);
+    int cum = __builtin_amdgcn_readlane(incl, 63) - incl;     // entries in the bins above
+    int low = 512;
+#pragma unroll
+    for (int j = 7; j >= 0; --j) {
+      cum += cb[j];
+      if (cum <= cap) low = 8 * lane_id() + j;
+    }
+    low = wave_reduce(low, OpMin());
+    // all above the cap within the top bin (a flood of near-equal keys):
+    // that bin's boundary, the region then over the cap
+    low = min(low, 511);
+    const uint64_t T = (uint64_t)(base + (uint32_t)low) << sh;
+    Tf = T > (uint64_t)lo ? (uint32_t)min(T, (uint64_t)0xFFFFFFFFu) : lo;
   }
-  if (t == 0) s_cnt = 0;
-  __syncthreads();
-  Tf = max(Tf, row0_reduce(w_tau[lw], OpMax()));
   const uint64_t thr64 = Tf <= 1u ? 0ull : d2key((double)key2f(Tf));
   for (int s = t; s < X.ns; s += WG) {
     const uint32_t hw = X.hword[s];
@@ -1507,11 +1635,13 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
     // the maximum of the slice's penalised values, and the sums against it
     my->m = Ms;
     my->sx = xok ? Sx : 0.0;
-    my->s = sum_ok ? Ss * exp2(Rb - Ms * kc) : Ss;
-    my->tol = tol;
+    my->sxtol = (float)(xtol * 1.001);
+    my->s = EXACT && exs ? Sx : (sum_ok ? Ss * exp2(Rb - Ms * kc) : Ss);
+    my->tol = EXACT && exs ? xtol * 1.001 : tol;
     my->best_v = 0; my->best_i = INT_MAX; my->nan_i = INT_MAX;
     my->tau = Tf; my->ncand = s_cnt;
-    my->flags = (ovf ? SF_OVERFLOW : 0) | (sum_ok ? 0 : SF_INEXACT) | (xok ? SF_EXACT : 0);
+    my->flags = (ovf ? SF_OVERFLOW : 0) | ((EXACT && exs ? xok : sum_ok) ? 0 : SF_INEXACT) |
+                (xok ? SF_EXACT : 0);
   }
   // The region finisher runs in slow_kernel, after the grid: a kernel
   // boundary makes the slices' records visible across XCDs without

@@ -149,3 +149,43 @@ def test_fused_and_slow_kernels_emulated_on_golden_small_rows():
                 assert is_margin(res), (c.name, int(ids[b]), res.token, res.diag)
                 margins.append(c.name)
     assert len(margins) <= 2, margins
+
+
+def _sliced_cases():
+    """Rows of a sliced launch (V = 40000: two slices of the fused kernel's
+    sliced variant): top-p rows without a penalty window or top-k (the split
+    exact normaliser), one with a top-k and one with a penalty window (the
+    full one), and a row whose large values all sit in its second slice."""
+    V = 40000
+    rng = np.random.default_rng(31)
+    base = dict(temperature=1.0, top_k=0, top_p=0.9, min_p=0.0, typical_p=1.0,
+                repetition_penalty=1.0, n_keep=0)
+    rows = []
+    for i, (kw, hist) in enumerate([
+            (dict(), []),
+            (dict(temperature=0.7, top_p=0.95), []),
+            (dict(temperature=0.8, top_k=50, top_p=0.9), []),
+            (dict(repetition_penalty=1.3), [int(t) for t in rng.integers(0, V, 200)]),
+            (dict(top_p=0.99), [])]):
+        x = rng.normal(0.0, 3.0, V).astype(np.float32)
+        if i == 4:
+            x[V // 2:] += 4.0
+        prm = dict(base, **kw, seed=int(rng.integers(0, 2**31)))
+        rows.append(cases.SamplerCase(f"sliced{i}", x, prm, hist))
+    return rows
+
+
+def test_sliced_top_p_rows_emulated():
+    cs = _sliced_cases()
+    with tempfile.TemporaryDirectory() as tmp:
+        (ids, st), = run_pipeline([cs], tmp)
+    for b, c in enumerate(cs):
+        u = np.random.default_rng(c.params["seed"]).random()
+        res = R.sample_row(c.logits, _params(c), c.hist, u, tie="spread")
+        assert int(st[b]) & 0xFF == res.status, (c.name, int(st[b]), res.status)
+        assert int(ids[b]) == res.token or is_margin(res), (c.name, int(ids[b]), res.token)
+    # the split normaliser decides rows 0 and 1 in the region finisher (no
+    # exact re-read, no multi-pass path); rows 2 and 3 keep the full one
+    FLAG_SLOW, FLAG_EXACT = 0x100, 0x200
+    assert all(int(st[b]) & (FLAG_SLOW | FLAG_EXACT) == 0 for b in (0, 1)), st
+    assert all(int(st[b]) & FLAG_EXACT for b in (2, 3)), st

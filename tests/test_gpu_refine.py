@@ -136,3 +136,26 @@ def test_tied_group_at_the_cut_takes_the_sorting_finisher(want_probs):
     assert not t.mismatches, t.mismatches[:5]
     assert np.array_equal(ids, [o.token for o in orc])
     assert not np.any(st & FLAG_SLOW), np.flatnonzero(st & FLAG_SLOW)
+
+
+def test_sliced_nucleus_rows_decided_by_the_split_normaliser():
+    """The config-2 rows (B = 64, four slices) with top_p 3e-7 (relative)
+    from one of the oracle's cumulative sums: within the streamed fp32
+    normaliser's bound (4e-6), outside the split one's (exact fp64 terms for
+    the buffered entries, the fp32 bound only on the small mass below the
+    wave thresholds).  The region finisher decides them without the exact
+    re-read, and the token equals the oracle's."""
+    w = W.nucleus()
+    rng = np.random.default_rng(25)
+    prms = _near_cut_rows(rng, w.logits, None, dict(temperature=1.0), 100, 1000, rel=3e-7)
+    u = rng.random(w.B)
+    _say(f"[gpu] split normaliser B={w.B} V={w.V}")
+    ids, st, probs = sample_host(w.logits, prms, None, None, u)
+    orc = [R.sample_row(w.logits[b], prms[b], None, float(u[b]), tie="spread")
+           for b in range(w.B)]
+    want = np.array([o.token for o in orc])
+    assert np.array_equal(ids, want), np.flatnonzero(ids != want)[:8]
+    assert not np.any(st & FLAG_SLOW), np.flatnonzero(st & FLAG_SLOW)
+    refined = int(np.count_nonzero(st & FLAG_EXACT))
+    _say(f"[gpu] split normaliser: {refined} of {w.B} rows re-read")
+    assert refined == 0, np.flatnonzero(st & FLAG_EXACT)
