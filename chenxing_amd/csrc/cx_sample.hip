@@ -197,10 +197,13 @@ __device__ __forceinline__ int next_chunk(CX_LDS int* counter) {
 // callee wait for every load in flight (the calling convention), which in
 // the stream would drain the wave's chunk pipeline.
 // The k-th largest of the wave's 128 values v1, v2 (two per lane), as
-// kth_of_lanes.
-__device__ __forceinline__ uint32_t kth_of_lanes2(uint32_t v1, uint32_t v2, int k) {
+// kth_of_lanes.  With stop > 0 only the key bits from stop up are
+// selected: the result is the k-th largest with its lower bits cleared, a
+// lower bound of it (the seeds, where a slightly lower first threshold
+// costs less than the full selection).
+__device__ __forceinline__ uint32_t kth_of_lanes2(uint32_t v1, uint32_t v2, int k, int stop = 0) {
   uint32_t prefix = 0u;
-  for (int sh = 30; sh >= 0; sh -= 2) {
+  for (int sh = 30; sh >= stop; sh -= 2) {
     const uint32_t b1 = prefix | (1u << sh), b2 = prefix | (2u << sh), b3 = prefix | (3u << sh);
     const int c3 = __popcll(ballot(v1 >= b3)) + __popcll(ballot(v2 >= b3));
     const int c2 = __popcll(ballot(v1 >= b2)) + __popcll(ballot(v2 >= b2));
@@ -209,9 +212,9 @@ __device__ __forceinline__ uint32_t kth_of_lanes2(uint32_t v1, uint32_t v2, int 
   }
   return prefix;
 }
-__device__ __forceinline__ uint32_t kth_of_lanes(uint32_t v, int k) {
+__device__ __forceinline__ uint32_t kth_of_lanes(uint32_t v, int k, int stop = 0) {
   uint32_t prefix = 0u;
-  for (int sh = 30; sh >= 0; sh -= 2) {
+  for (int sh = 30; sh >= stop; sh -= 2) {
     const uint32_t b1 = prefix | (1u << sh), b2 = prefix | (2u << sh), b3 = prefix | (3u << sh);
     const int c3 = __popcll(ballot(v >= b3));
     const int c2 = __popcll(ballot(v >= b2));
@@ -1302,8 +1305,10 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   CX_LDS uint32_t* const lpub = to_lds(w_pub);
 
   // seed: every lane's largest unpenalised element of its first chunk (a
-  // vector's NE penalty bits sit in one bitmap word: one LDS read each)
-  uint32_t ck = 0u;
+  // vector's NE penalty bits sit in one bitmap word: one LDS read each),
+  // and for wide rows (below) its second largest, in the same pass
+  uint32_t ck = 0u, c2 = 0u;
+  const bool two = krow > 64 && pub_r >= 32;
   if (wave_id() * CH < nv) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -1315,6 +1320,7 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
       for (int j = 0; j < NE; ++j) {
         const bool ok = vi < nv && x[j] == x[j] && !((pb >> j) & 1u);
         const uint32_t k = ok ? f2key(x[j]) : 0u;
+        if (two) c2 = k > ck ? ck : (k > c2 ? k : c2);
         ck = k > ck ? k : ck;
       }
     }
@@ -1326,32 +1332,16 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   // above it).  (A wave's own lane values alone give a threshold too low to
   // keep the first chunks' appends cheap, and with r = 64 the lane maxima
   // alone give their smallest.)
+  // (The selections stop at the keys' upper 16 bits: sign, exponent and 7
+  // mantissa bits, a threshold lower by at most 1/128 of its magnitude.)
   if (krow <= 64) {
     publish_top(ck, NSLOT, lslots + NSLOT * wave_id());
     __syncthreads();
-    raise_tau(wb, kth_of_lanes(lds_load(lslots + lane_id()), krow));
+    raise_tau(wb, kth_of_lanes(lds_load(lslots + lane_id()), krow, 16));
   } else if (pub_r > 0) {
-    // for r of 32 and more, the lanes' second largest values of the same
-    // chunk too (for smaller r the r-th largest lane maximum is already
-    // high, and the extra pass costs more than it saves)
-    uint32_t c1 = 0u, c2 = 0u;
-    if (pub_r >= 32 && wave_id() * CH < nv) {
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int vi = wave_id() * CH + u * 64 + lane_id();
-        float x[NE];
-        E::unpack(q[u], x);
-        const uint32_t pb = pen_bits<NE>(X, pen_on && vi < nv, vi * NE);
-#pragma unroll
-        for (int j = 0; j < NE; ++j) {
-          const bool ok = vi < nv && x[j] == x[j] && !((pb >> j) & 1u);
-          const uint32_t k = ok ? f2key(x[j]) : 0u;
-          c2 = k > c1 ? c1 : (k > c2 ? k : c2);
-          c1 = k > c1 ? k : c1;
-        }
-      }
-    }
-    const uint32_t th = pub_r >= 32 ? kth_of_lanes2(c1, c2, pub_r) : kth_of_lanes(ck, pub_r);
+    // for r of 32 and more, the lanes' second largest values too (for
+    // smaller r the r-th largest lane maximum is already high)
+    const uint32_t th = two ? kth_of_lanes2(ck, c2, pub_r, 16) : kth_of_lanes(ck, pub_r, 16);
     if (lane_id() == 0) lpub[wave_id()] = th;
     __syncthreads();
     raise_tau(wb, pub_min(lpub));
