@@ -386,9 +386,29 @@ __device__ inline int finish_row_fast(const SampleArgs& A, int row, const cx_row
   __shared__ int f_n;
   __shared__ int f_j;
   __shared__ int f_g[2];
+  __shared__ SplitStats s_st[SLICE_CAP];
   const int t = threadIdx.x;
   const int nsp = A.nsplit;
-  const SplitStats* st = A.stats + (size_t)row * nsp;
+  const SplitStats* gst = A.stats + (size_t)row * nsp;
+  // Every load at once, before anything waits: the slices' records (one
+  // thread each, into LDS) and the candidates where the usual layout puts
+  // them, entry g of this thread's R at slice g / C, position g % C (C: a
+  // slice's share of the capacity).  Entries past a slice's count are read
+  // (the workspace holds CAPS per slice) and dropped below.
+  const int C = CAP / nsp;
+  Cand c[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int g = r * WG + t;
+    const int s = g / C;
+    c[r].key = 0ull;
+    c[r].idx = 0;
+    if (s < nsp) c[r] = A.cands[((size_t)row * nsp + s) * CAPS + (g - s * C)];
+  }
+  if (t < nsp) s_st[t] = gst[t];
+  if (t == 0) f_n = 0;
+  __syncthreads();
+  const SplitStats* st = s_st;
   int flags = 0;
   for (int s = 0; s < nsp; ++s) flags |= st[s].flags;
 
@@ -464,37 +484,28 @@ __device__ inline int finish_row_fast(const SampleArgs& A, int row, const cx_row
   double* sv = (double*)(dyn + CAP * 16);
   double* sc = sv + CAP;
 
-  // the slices' candidates as one list (prefix of their counts), so their
-  // loads go out together rather than one slice after another
-  __shared__ int f_off[SLICE_CAP + 1];
-  if (t == 0) {
-    int o = 0;
-    for (int s = 0; s < nsp; ++s) { f_off[s] = o; o += st[s].ncand; }
-    f_off[nsp] = o;
-    f_n = 0;
+  // the loaded candidates at or above the threshold into the region list
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int g = r * WG + t;
+    const int s = g / C;
+    const bool p = s < nsp && g - s * C < st[s].ncand && c[r].key >= thr64;
+    const int pos = wave_append_slot(p, &f_n);
+    if (p && pos < CAP) { skey[pos] = c[r].key; sidx[pos] = c[r].idx; saux[pos] = 0; }
   }
-  __syncthreads();
-  const int ncand = f_off[nsp];
-  // R candidates per thread per round, their loads issued together (uniform
-  // trips: whole waves append)
-  for (int g0 = 0; g0 < ncand; g0 += R * WG) {
-    Cand c[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int g = g0 + r * WG + t;
-      c[r].key = 0ull;
-      c[r].idx = 0;
-      if (g < ncand) {
-        int s = 0;
-        while (g >= f_off[s + 1]) ++s;
-        c[r] = A.cands[((size_t)row * nsp + s) * CAPS + (g - f_off[s])];
-      }
-    }
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const bool p = g0 + r * WG + t < ncand && c[r].key >= thr64;
+  // a slice holding more than C candidates (a flood of ties past the
+  // threshold): the rest, slice by slice
+  for (int s = 0; s < nsp; ++s) {
+    const int n = st[s].ncand;
+    for (int e0 = C; e0 < n; e0 += WG) {
+      const int e = e0 + t;
+      Cand cc;
+      cc.key = 0ull;
+      cc.idx = 0;
+      if (e < n) cc = A.cands[((size_t)row * nsp + s) * CAPS + e];
+      const bool p = e < n && cc.key >= thr64;
       const int pos = wave_append_slot(p, &f_n);
-      if (p && pos < CAP) { skey[pos] = c[r].key; sidx[pos] = c[r].idx; saux[pos] = 0; }
+      if (p && pos < CAP) { skey[pos] = cc.key; sidx[pos] = cc.idx; saux[pos] = 0; }
     }
   }
   __syncthreads();

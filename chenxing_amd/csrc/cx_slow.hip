@@ -61,17 +61,21 @@ __global__ __launch_bounds__(WG) void slow_kernel(SampleArgs A) {
   __shared__ int s_state;
   enum { DECIDED, MULTIPASS, REFINE, FINISH };
   const int row = (int)blockIdx.x;
-  if (threadIdx.x == 0) {
-    // a sliced row's status word is not written by the fused kernel
-    const int st = A.row_status[row];
-    s_state = A.pending_only ? (st == ROW_PENDING ? MULTIPASS : DECIDED)
-              : A.all_slow ? MULTIPASS
-              : (A.nsplit > 1 || st == ROW_FINISH) ? FINISH
-              : st == ROW_PENDING ? MULTIPASS
-              : st == ROW_REFINE ? REFINE : DECIDED;
+  int state = FINISH;
+  // a sliced row's status word is not written by the fused kernel: every
+  // sliced row is finished here, with no load before the finisher's own
+  if (A.pending_only || A.all_slow || A.nsplit == 1) {
+    if (threadIdx.x == 0) {
+      const int st = A.row_status[row];
+      s_state = A.pending_only ? (st == ROW_PENDING ? MULTIPASS : DECIDED)
+                : A.all_slow ? MULTIPASS
+                : st == ROW_FINISH ? FINISH
+                : st == ROW_PENDING ? MULTIPASS
+                : st == ROW_REFINE ? REFINE : DECIDED;
+    }
+    __syncthreads();
+    state = s_state;
   }
-  __syncthreads();
-  int state = s_state;
   if (state == DECIDED) return;
   if (state == FINISH) {
     const cx_row_params P = A.prm[row];
