@@ -234,7 +234,7 @@ __device__ inline int finish_bucketed(const SampleArgs& A, int row, const cx_row
                                       const uint64_t* skey, const int32_t* sidx, int32_t* kf,
                                       double* sv, double* sc, int E, bool region_all, double M,
                                       double invT, double S, double tol, bool exact,
-                                      double* red_d, int* red_i) {
+                                      double* red_d, int* red_i, const double* tab) {
   __shared__ PrefixCut pc;
   __shared__ int s_ctr[6];                           // per cut: gather count, cut bucket
   const int t = threadIdx.x;
@@ -254,7 +254,7 @@ __device__ inline int finish_bucketed(const SampleArgs& A, int row, const cx_row
   uint64_t kmax = 0ull, kmin = ~0ull;
   for (int j = t; j < E; j += WG) {
     const uint64_t k = skey[j];
-    sv[j] = exp((key2d(k) - M) * invT) / S;
+    sv[j] = exp64_neg((key2d(k) - M) * invT, tab) / S;     // within 1 ulp, as exp
     kf[j] = 1;
     kmax = k > kmax ? k : kmax;
     kmin = k < kmin ? k : kmin;
@@ -387,6 +387,7 @@ __device__ inline int finish_row_fast(const SampleArgs& A, int row, const cx_row
   __shared__ int f_j;
   __shared__ int f_g[2];
   __shared__ SplitStats s_st[SLICE_CAP];
+  __shared__ double f_tab[64];                       // EXP64_TAB
   const int t = threadIdx.x;
   const int nsp = A.nsplit;
   const SplitStats* gst = A.stats + (size_t)row * nsp;
@@ -406,11 +407,16 @@ __device__ inline int finish_row_fast(const SampleArgs& A, int row, const cx_row
     if (s < nsp) c[r] = A.cands[((size_t)row * nsp + s) * CAPS + (g - s * C)];
   }
   if (t < nsp) s_st[t] = gst[t];
+  if (t < 64) f_tab[t] = EXP64_TAB[t];
   if (t == 0) f_n = 0;
   __syncthreads();
   const SplitStats* st = s_st;
-  int flags = 0;
-  for (int s = 0; s < nsp; ++s) flags |= st[s].flags;
+  // the row's scalars, lane s of row 0 taking slice s (every wave; one
+  // exponential per lane, not one per slice in turn)
+  const int ls = lane_id() & 15;
+  const bool lin = ls < nsp;
+  const SplitStats& me = st[lin ? ls : 0];
+  const int flags = row0_reduce(lin ? me.flags : 0, OpOr());
 
   if (flags & SF_UNSUPPORTED) {
     write_row_result(A, row, CX_ROW_UNSUPPORTED, -1);
@@ -430,20 +436,12 @@ __device__ inline int finish_row_fast(const SampleArgs& A, int row, const cx_row
   }
 
   const double invT = 1.0 / P.temperature;
-  double M = -__builtin_inf();
-  bool mnan = false;
-  for (int s = 0; s < nsp; ++s) {
-    mnan |= st[s].m != st[s].m;
-    M = st[s].m > M ? st[s].m : M;
-  }
-  double S = 0.0;
-  uint32_t tau = 1u;
-  double tol = TOL_S;
-  for (int s = 0; s < nsp; ++s) {
-    if (st[s].s != 0.0) S += st[s].s * exp((st[s].m - M) * invT);
-    tau = max(tau, st[s].tau);
-    tol = st[s].tol > tol ? st[s].tol : tol;
-  }
+  const bool mnan = row0_reduce(lin && me.m != me.m ? 1 : 0, OpOr()) != 0;
+  const double M = row0_reduce(lin && me.m == me.m ? me.m : -__builtin_inf(), OpMax());
+  const double f = lin ? exp((me.m - M) * invT) : 0.0;       // slice s's sums to M
+  double S = row0_reduce(lin && me.s != 0.0 ? me.s * f : 0.0, OpAdd());
+  const uint32_t tau = row0_reduce(lin ? me.tau : 1u, OpMax());
+  double tol = row0_reduce(lin && me.tol > TOL_S ? me.tol : TOL_S, OpMax());
   bool exact = S_exact > 0.0;
   if (exact) {
     S = S_exact;
@@ -451,16 +449,11 @@ __device__ inline int finish_row_fast(const SampleArgs& A, int row, const cx_row
     // the slices' fp64 sums (sliced top-p rows), when every slice has one:
     // S = sum over slices of sx_s exp((m_s - M) / T), exact when every
     // slice's is, else within the slices' bounds (split sums)
-    bool allx = true;
-    double Sx = 0.0, Bx = 0.0;
-    for (int s = 0; s < nsp; ++s) {
-      allx = allx && (st[s].flags & SF_EXACT);
-      if ((st[s].flags & SF_EXACT) && st[s].sx != 0.0) {
-        const double v = st[s].sx * exp((st[s].m - M) * invT);
-        Sx += v;
-        Bx += (double)st[s].sxtol * v;
-      }
-    }
+    const bool mx = lin && (me.flags & SF_EXACT);
+    const bool allx = row0_reduce(lin && !mx ? 1 : 0, OpOr()) == 0;
+    const double v = mx && me.sx != 0.0 ? me.sx * f : 0.0;
+    const double Sx = row0_reduce(v, OpAdd());
+    const double Bx = row0_reduce((double)(mx ? me.sxtol : 0.0f) * v, OpAdd());
     if (allx && Sx > 0.0 && Sx < __builtin_inf()) {
       S = Sx;
       if (Bx == 0.0) exact = true;
@@ -541,7 +534,7 @@ __device__ inline int finish_row_fast(const SampleArgs& A, int row, const cx_row
   const bool region_all = region_all_pre && !region_incomplete_after_shrink;
   {
     const int rb = finish_bucketed(A, row, P, skey, sidx, saux, sv, sc, E, region_all, M, invT, S,
-                                   tol, exact, red_d, red_i);
+                                   tol, exact, red_d, red_i, f_tab);
     if (rb != FIN_SORTED) return rb;
   }
   // a cut's bucket overflowed (near-equal values): sort the region instead
