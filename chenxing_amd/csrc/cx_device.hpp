@@ -168,6 +168,21 @@ __device__ __forceinline__ double wave_scan_dpp(double v) {
   v += dpp_update0<0x143, 0xC>(v);   // row_bcast:31 into rows 2 and 3
   return v;
 }
+template <int CTRL, int ROWS>
+__device__ __forceinline__ unsigned long long dpp_update0(unsigned long long b) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, CTRL, ROWS, 0xF, true);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), CTRL, ROWS, 0xF, true);
+  return ((unsigned long long)hi << 32) | lo;
+}
+__device__ __forceinline__ unsigned long long wave_scan_dpp(unsigned long long v) {
+  v += dpp_update0<0x111, 0xF>(v);
+  v += dpp_update0<0x112, 0xF>(v);
+  v += dpp_update0<0x114, 0xF>(v);
+  v += dpp_update0<0x118, 0xF>(v);
+  v += dpp_update0<0x142, 0xA>(v);
+  v += dpp_update0<0x143, 0xC>(v);
+  return v;
+}
 __device__ __forceinline__ int wave_scan_dpp(int v) {
   v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, true);
   v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, true);

@@ -95,15 +95,6 @@ constexpr int NBK = WG;            // buckets: one per thread in the scan
 constexpr int GBK = 64;            // a gathered bucket: one entry per lane
 constexpr double FX_MASS = 1152921504606846976.0;   // 2^60: masses sum to <= ~1
 
-// Inclusive prefix sum across the 64 lanes (integers).
-__device__ __forceinline__ unsigned long long wave_incl_scan_u64(unsigned long long v) {
-  for (int o = 1; o < 64; o <<= 1) {
-    const unsigned long long w = __shfl_up(v, o);
-    if (lane_id() >= o) v += w;
-  }
-  return v;
-}
-
 struct PrefixCut {
   int found;        // the running weight reaches the target inside the entries
   int overflow;     // the cut's bucket holds more than GBK entries
@@ -141,7 +132,7 @@ __device__ inline void prefix_cut(int E, const int32_t* sidx, BucketOf bucket_of
   // exclusive scan of the buckets (thread t owns bucket t): every thread
   // reads the waves' totals, so the scan across waves costs no barrier
   const unsigned long long mine = bm[t];
-  const unsigned long long inc = wave_incl_scan_u64(mine);
+  const unsigned long long inc = wave_scan_dpp(mine);
   if (lane_id() == 63) red_u[wave_id()] = inc;
   __syncthreads();
   unsigned long long wbase = 0ull, all = 0ull;
@@ -189,11 +180,25 @@ __device__ inline void prefix_cut(int E, const int32_t* sidx, BucketOf bucket_of
   }
   if (wave_id() == 0) {
     const int l = lane_id();
+    // the bucket's n entries in rec_before order: each lane's rank among
+    // them (n is usually a few, so n broadcast reads beat a 64-wide
+    // sorting network), then each entry written at its rank and read back
     Rec r[1];
     r[0].key = l < n ? gk[l] : 0ull;
     r[0].idx = l < n ? gi[l] : INT_MAX;
     r[0].aux = l < n ? ga[l] : -1;
-    wave_sort<1>(r);
+    int rank = 0;
+    for (int j = 0; j < n; ++j) {
+      const uint64_t kj = gk[j];
+      const int32_t ij = gi[j];
+      rank += (kj > r[0].key || (kj == r[0].key && ij < r[0].idx)) ? 1 : 0;
+    }
+    // every lane's reads above precede the writes (one wave's LDS
+    // operations complete in order; the barriers keep the compiler's order)
+    __builtin_amdgcn_wave_barrier();
+    if (l < n) { gk[rank] = r[0].key; gi[rank] = r[0].idx; ga[rank] = r[0].aux; }
+    __builtin_amdgcn_wave_barrier();
+    if (l < n) { r[0].key = gk[l]; r[0].idx = gi[l]; r[0].aux = ga[l]; }
     const double w = l < n ? weight(r[0].aux) : 0.0;
     const double incl = wave_scan_dpp(w);
     if (l < n) ga[l] = r[0].aux;
