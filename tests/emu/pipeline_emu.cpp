@@ -11,6 +11,8 @@
 // the run.  The hand-off between the kernels (row status, hand-off marks,
 // slice records, regions) is the fused kernel's own output.
 // usage: pipeline_emu IN OUT   (written and read by tests/test_emu_pipeline.py)
+// The layouts restated below follow cx_api.hip (slow_layout, fused_layout,
+// plan_nsplit).
 #include <string>
 #include "cx_device.hpp"
 #include "cx_internal.hpp"
@@ -91,6 +93,9 @@ static void fused_layout(SampleArgs& A, int64_t ldh) {
 }
 constexpr int FUSED_LDS_MAX = 150 * 1024;
 static int plan_nsplit(int B, int V, int64_t ldh) {
+  // EMU_NSPLIT: force the slice count (long single-slice rows without the
+  // batch of 256 rows that gives them)
+  if (getenv("EMU_NSPLIT")) return atoi(getenv("EMU_NSPLIT"));
   SampleArgs A;
   memset(&A, 0, sizeof A);
   slow_layout(A, V, ldh);

@@ -89,7 +89,7 @@ def _params(c) -> RowParams:
                      repetition_penalty=p["repetition_penalty"], n_keep=p["n_keep"])
 
 
-def run_pipeline(groups_in, tmp):
+def run_pipeline(groups_in, tmp, env=None):
     """groups_in: list of case lists (one V each).  Returns [(ids, status)]."""
     exe = _build(tmp)
     fin, fout = os.path.join(tmp, "in.bin"), os.path.join(tmp, "out.bin")
@@ -112,7 +112,8 @@ def run_pipeline(groups_in, tmp):
                 f.write(hl.tobytes())
             u = np.array([np.random.default_rng(c.params["seed"]).random() for c in cs])
             f.write(u.astype(np.float64).tobytes())
-    r = subprocess.run([exe, fin, fout], capture_output=True, text=True, timeout=1500)
+    r = subprocess.run([exe, fin, fout], capture_output=True, text=True, timeout=1500,
+                       env=dict(os.environ, **(env or {})))
     assert r.returncode == 0, r.stderr[-6000:]
     out = open(fout, "rb").read()
     res, off = [], 0
@@ -189,3 +190,29 @@ def test_sliced_top_p_rows_emulated():
     FLAG_SLOW, FLAG_EXACT = 0x100, 0x200
     assert all(int(st[b]) & (FLAG_SLOW | FLAG_EXACT) == 0 for b in (0, 1)), st
     assert all(int(st[b]) & FLAG_EXACT for b in (2, 3)), st
+
+
+def test_long_single_slice_rows_emulated():
+    """Single-slice rows of 50000 elements (49 chunks, so the LDS chunk
+    counter hands out chunks past the first two per wave; the slice count is
+    forced to 1, as a batch of 256 rows would give): a top-k + top-p row, a
+    nucleus row and a penalised row."""
+    V = 50000
+    rng = np.random.default_rng(37)
+    base = dict(temperature=0.8, top_k=0, top_p=0.9, min_p=0.0, typical_p=1.0,
+                repetition_penalty=1.0, n_keep=0)
+    rows = []
+    for i, (kw, hist) in enumerate([
+            (dict(top_k=40), []),
+            (dict(top_p=0.95, temperature=1.0), []),
+            (dict(top_k=50, repetition_penalty=1.2), [int(t) for t in rng.integers(0, V, 300)])]):
+        x = rng.normal(0.0, 3.0, V).astype(np.float32)
+        rows.append(cases.SamplerCase(f"long{i}", x, dict(base, **kw, seed=int(rng.integers(0, 2**31))),
+                                      hist))
+    with tempfile.TemporaryDirectory() as tmp:
+        (ids, st), = run_pipeline([rows], tmp, env={"EMU_NSPLIT": "1"})
+    for b, c in enumerate(rows):
+        u = np.random.default_rng(c.params["seed"]).random()
+        res = R.sample_row(c.logits, _params(c), c.hist, u, tie="spread")
+        assert int(st[b]) & 0xFF == res.status, (c.name, int(st[b]), res.status)
+        assert int(ids[b]) == res.token or is_margin(res), (c.name, int(ids[b]), res.token)
