@@ -1492,60 +1492,66 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   // ---- combine: S = sum over waves of 2^(Rw - Rb) s_w + 2^(Rc_w - Rb) corr_w
   const float Rl = w_R[lw];
   const double Rcl = s_pen[lw].Rc;
-  const float Rf = row0_reduce(Rl, OpMax());
   uint32_t Tf = row0_reduce(w_tau[lw], OpMax());
   const uint32_t kmx = row0_reduce(w_kmx[lw], OpMax());
   const int flw = row0_reduce(w_fl[lw] | s_pen[lw].fl, OpOr());
   const int anynan = flw & 1, ovf = flw & 2;
   if (krow <= 64) Tf = max(Tf, kth_of_lanes(lds_load(lslots + lane_id()), krow));
-  const double PMX = row0_reduce(s_pen[lw].pmx, OpMax());
-  const double Rb = fmax((double)Rf, row0_reduce(Rcl, OpMax()));
-  // an exponent offset past +-2^22 leaves fp32 term arguments inexact
-  const bool rb_ok = Rf > -__builtin_inff() && fabs(Rb) < 4194304.0;
-  double Ss = 0.0, PR = 0.0;
-  if (rb_ok) {
-    const double sw = w_s[lw];
-    const double cw = s_pen[lw].corr, pw = s_pen[lw].pr;
-    const int dc = (int)fmax(Rcl - Rb, -2048.0);
-    const double term = (sw != 0.0 ? __builtin_ldexp(sw, (int)fmax((double)Rl - Rb, -2048.0)) : 0.0) +
-                        (cw != 0.0 ? __builtin_ldexp(cw, dc) : 0.0);
-    Ss = row0_reduce(term, OpAdd());
-    PR = row0_reduce(pw != 0.0 ? __builtin_ldexp(pw, dc) : 0.0, OpAdd());
-  }
-  const double tol = TOL_S + 2.0 * TOL_T * PR / Ss;
-  const bool sum_ok = !anynan && rb_ok && Ss > 0.0 && Ss < __builtin_inf() && tol <= TOL_MAX;
-  // the slice's exact fp64 normaliser against its maximum Ms: the waves' sums
-  // and their penalty corrections, each rescaled to Ms (lane w of each row of
-  // 16 lanes takes wave w).  Kept where the raw terms the corrections
-  // replace are not so large that cancelling them loses the sum's precision.
-  const double Mu = kmx ? (double)key2f(kmx) : -__builtin_inf();
-  const double Ms = Mu > PMX ? Mu : PMX;
-  double Sx = 0.0, xtol = 0.0;
-  bool xok = false;
-  if (EXACT && ex && sum_ok && Ms > -__builtin_inf() && Ms < __builtin_inf()) {
-    const double f = s_pen[lw].refx > -__builtin_inf()
-                         ? exp64_neg((s_pen[lw].refx - Ms) * invT, etab) : 0.0;
-    const double ws = w_xs[lw];
-    const double term = (ws != 0.0 ? ws * exp64_neg((w_xm[lw] - Ms) * invT, etab) : 0.0) +
-                        s_pen[lw].corrx * f;
-    Sx = row0_reduce(term, OpAdd());
-    const double PRx = row0_reduce(s_pen[lw].prx * f, OpAdd());
-    xok = Sx > 0.0 && Sx < __builtin_inf() && PRx < 1e5 * Sx;
-  }
-  if (EXACT && exs && !anynan && rb_ok && !(flw & 4) && Ss < __builtin_inf() &&
-      Ms > -__builtin_inf() && Ms < __builtin_inf()) {
-    // split (Ss holds only the below-threshold terms, and may be 0): the
-    // buffered entries' exact terms plus the below-threshold ones, both
-    // against Ms; the bound is TOL_S of the latter (with a margin for the
-    // fp64 roundings of the sums)
-    const double ws = w_xs[lw];
-    const double Sa = row0_reduce(ws != 0.0 ? ws * exp64_neg((w_xm[lw] - Ms) * invT, etab) : 0.0,
-                                  OpAdd());
-    const double Stm = Ss != 0.0 ? Ss * exp2(Rb - Ms * kc) : 0.0;
-    Sx = Sa + Stm;
-    xok = Sx > 0.0 && Sx < __builtin_inf();
-    xtol = xok ? TOL_S * Stm / Sx + 1e-12 : 0.0;
-  }
+  // The slice's sums for its record are taken by wave 0 alone, after its
+  // share of the region (below): the other waves need only Tf and kmx.
+  double Ss = 0.0, tol = 0.0, Rb = 0.0, Ms = 0.0, Sx = 0.0, xtol = 0.0;
+  bool sum_ok = false, xok = false;
+  auto slice_sums = [&]() {
+    const float Rf = row0_reduce(Rl, OpMax());
+    const double PMX = row0_reduce(s_pen[lw].pmx, OpMax());
+    Rb = fmax((double)Rf, row0_reduce(Rcl, OpMax()));
+    // an exponent offset past +-2^22 leaves fp32 term arguments inexact
+    const bool rb_ok = Rf > -__builtin_inff() && fabs(Rb) < 4194304.0;
+    double PR = 0.0;
+    if (rb_ok) {
+      const double sw = w_s[lw];
+      const double cw = s_pen[lw].corr, pw = s_pen[lw].pr;
+      const int dc = (int)fmax(Rcl - Rb, -2048.0);
+      const double term =
+          (sw != 0.0 ? __builtin_ldexp(sw, (int)fmax((double)Rl - Rb, -2048.0)) : 0.0) +
+          (cw != 0.0 ? __builtin_ldexp(cw, dc) : 0.0);
+      Ss = row0_reduce(term, OpAdd());
+      PR = row0_reduce(pw != 0.0 ? __builtin_ldexp(pw, dc) : 0.0, OpAdd());
+    }
+    tol = TOL_S + 2.0 * TOL_T * PR / Ss;
+    sum_ok = !anynan && rb_ok && Ss > 0.0 && Ss < __builtin_inf() && tol <= TOL_MAX;
+    // the slice's exact fp64 normaliser against its maximum Ms: the waves'
+    // sums and their penalty corrections, each rescaled to Ms (lane w of
+    // each row of 16 lanes takes wave w).  Kept where the raw terms the
+    // corrections replace are not so large that cancelling them loses the
+    // sum's precision.
+    const double Mu = kmx ? (double)key2f(kmx) : -__builtin_inf();
+    Ms = Mu > PMX ? Mu : PMX;
+    if (EXACT && ex && sum_ok && Ms > -__builtin_inf() && Ms < __builtin_inf()) {
+      const double f = s_pen[lw].refx > -__builtin_inf()
+                           ? exp64_neg((s_pen[lw].refx - Ms) * invT, etab) : 0.0;
+      const double ws = w_xs[lw];
+      const double term = (ws != 0.0 ? ws * exp64_neg((w_xm[lw] - Ms) * invT, etab) : 0.0) +
+                          s_pen[lw].corrx * f;
+      Sx = row0_reduce(term, OpAdd());
+      const double PRx = row0_reduce(s_pen[lw].prx * f, OpAdd());
+      xok = Sx > 0.0 && Sx < __builtin_inf() && PRx < 1e5 * Sx;
+    }
+    if (EXACT && exs && !anynan && rb_ok && !(flw & 4) && Ss < __builtin_inf() &&
+        Ms > -__builtin_inf() && Ms < __builtin_inf()) {
+      // split (Ss holds only the below-threshold terms, and may be 0): the
+      // buffered entries' exact terms plus the below-threshold ones, both
+      // against Ms; the bound is TOL_S of the latter (with a margin for the
+      // fp64 roundings of the sums)
+      const double ws = w_xs[lw];
+      const double Sa = row0_reduce(
+          ws != 0.0 ? ws * exp64_neg((w_xm[lw] - Ms) * invT, etab) : 0.0, OpAdd());
+      const double Stm = Ss != 0.0 ? Ss * exp2(Rb - Ms * kc) : 0.0;
+      Sx = Sa + Stm;
+      xok = Sx > 0.0 && Sx < __builtin_inf();
+      xtol = xok ? TOL_S * Stm / Sx + 1e-12 : 0.0;
+    }
+  };
 
   // ---- general: bound the region, write it and the statistics, then finish
   // The region is every buffered entry at or above T, and every element at
@@ -1620,6 +1626,7 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
       }
     }
   }
+  if (wave_id() == 0) slice_sums();
   __syncthreads();
   if (t == 0) {
     // the maximum of the slice's penalised values, and the sums against it
