@@ -399,9 +399,15 @@ __device__ inline int finish_row_fast(const SampleArgs& A, int row, const cx_row
   // Every load at once, before anything waits: the slices' records (one
   // thread each, into LDS) and the candidates where the usual layout puts
   // them, entry g of this thread's R at slice g / C, position g % C (C: a
-  // slice's share of the capacity).  Entries past a slice's count are read
-  // (the workspace holds CAPS per slice) and dropped below.
-  const int C = CAP / nsp;
+  // slice's share of the capacity, at most one entry per thread, so a
+  // single-slice row reads ahead 16 KB, not its whole 64 KB share).
+  // Entries past a slice's count are read (the workspace holds CAPS per
+  // slice) and dropped below.
+  const int C = min(CAP / nsp, WG);
+  if (t < nsp) s_st[t] = gst[t];
+  if (t < 64) f_tab[t] = EXP64_TAB[t];
+  // (a greedy row reads no candidates: its parameters come first)
+  const bool stoch = P.temperature != 0.0;
   Cand c[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
@@ -409,10 +415,8 @@ __device__ inline int finish_row_fast(const SampleArgs& A, int row, const cx_row
     const int s = g / C;
     c[r].key = 0ull;
     c[r].idx = 0;
-    if (s < nsp) c[r] = A.cands[((size_t)row * nsp + s) * CAPS + (g - s * C)];
+    if (stoch && s < nsp) c[r] = A.cands[((size_t)row * nsp + s) * CAPS + (g - s * C)];
   }
-  if (t < nsp) s_st[t] = gst[t];
-  if (t < 64) f_tab[t] = EXP64_TAB[t];
   if (t == 0) f_n = 0;
   __syncthreads();
   const SplitStats* st = s_st;
