@@ -129,35 +129,48 @@ __device__ inline void prefix_cut(int E, const int32_t* sidx, BucketOf bucket_of
   for (int j = t; j < E; j += WG)
     if (elig(j)) atomicAdd(&bm[bucket_of(j)], (unsigned long long)(weight(j) * scale));
   __syncthreads();
-  // exclusive scan of the buckets (thread t owns bucket t): every thread
-  // reads the waves' totals, so the scan across waves costs no barrier
-  const unsigned long long mine = bm[t];
-  const unsigned long long inc = wave_scan_dpp(mine);
-  if (lane_id() == 63) red_u[wave_id()] = inc;
-  __syncthreads();
-  unsigned long long wbase = 0ull, all = 0ull;
+  // the cut bucket, by wave 0 alone (lane l scans buckets 16 l .. 16 l + 15
+  // and a DPP scan carries the lanes' totals): the first bucket whose running
+  // weight reaches the target.  The running weight is monotone, so that
+  // bucket is nonempty and the one whose weight before it does not reach
+  // the target.
+  if (wave_id() == 0) {
+    constexpr int PB = NBK / 64;
+    const int l = lane_id();
+    unsigned long long bw[PB];
+    unsigned long long lsum = 0ull;
 #pragma unroll
-  for (int w = 0; w < NWAVE; ++w) {
-    const unsigned long long x = red_u[w];
-    wbase += w < wave_id() ? x : 0ull;
-    all += x;
-  }
-  const unsigned long long base = wbase + (inc - mine);
-  const double total = (double)all / scale;
-  const double tgt = relative ? target * total : target;
-  const double be = (double)(base + mine) / scale;
-  const bool hit = mine != 0ull && (strict ? be > tgt : be >= tgt);
-  // The running weight is monotone, so the first bucket that reaches the
-  // target is the one nonempty bucket whose weight before it does not: the
-  // last nonempty bucket before it ends at that weight.  Its thread claims
-  // it (no block-wide minimum).
-  const double bp = (double)base / scale;
-  const bool before = base != 0ull && (strict ? bp > tgt : bp >= tgt);
-  if (hit && !before) {
-    pc_bc = t;
-    red_u[2 * NWAVE + 1] = base;                     // the weight before the cut bucket
+    for (int i = 0; i < PB; ++i) {
+      bw[i] = bm[l * PB + i];
+      lsum += bw[i];
+    }
+    const unsigned long long incl = wave_scan_dpp(lsum);
+    const unsigned long long all = lane_read((uint64_t)incl, 63);
+    const double total = (double)all / scale;
+    const double tgt = relative ? target * total : target;
+    unsigned long long run = incl - lsum;              // weight before the lane's buckets
+    int first = INT_MAX;
+    unsigned long long before = 0ull;
+#pragma unroll
+    for (int i = 0; i < PB; ++i) {
+      const unsigned long long bi = run;
+      run += bw[i];
+      const double be = (double)run / scale;
+      if (first == INT_MAX && bw[i] != 0ull && (strict ? be > tgt : be >= tgt)) {
+        first = l * PB + i;
+        before = bi;
+      }
+    }
+    const uint64_t hb = ballot(first != INT_MAX);
+    if (hb) {
+      const int fl = __builtin_ctzll(hb);
+      if (l == fl) { pc_bc = first; red_u[2 * NWAVE + 1] = before; }
+    }
+    if (l == 0) red_d[2 * NWAVE + 2] = total;
   }
   __syncthreads();
+  const double total = red_d[2 * NWAVE + 2];
+  const double tgt = relative ? target * total : target;
   const int bc = pc_bc;
   if (bc == INT_MAX) {
     if (t == 0) { out.found = 0; out.overflow = 0; out.total = total; }
