@@ -252,45 +252,31 @@ __device__ inline int finish_bucketed(const SampleArgs& A, int row, const cx_row
                                       const uint64_t* skey, const int32_t* sidx, int32_t* kf,
                                       double* sv, double* sc, int E, bool region_all, double M,
                                       double invT, double S, double tol, bool exact,
-                                      double* red_d, int* red_i, const double* tab) {
+                                      double* red_d, int* red_i, const double* tab,
+                                      const uint64_t* ext, int* s_ctr) {
   __shared__ PrefixCut pc;
-  __shared__ int s_ctr[6];                           // per cut: gather count, cut bucket
   const int t = threadIdx.x;
   // the gathered bucket, then the buckets of the three cuts (top-k, top-p,
-  // draw), all cleared here, before the barrier below
+  // draw); the caller cleared the buckets and s_ctr (per cut: gather count,
+  // cut bucket) and posted the waves' extremes (ext) before its barrier
   uint64_t* gk = (uint64_t*)sc;
   int32_t* gi = (int32_t*)(gk + GBK);
   int32_t* ga = gi + GBK;
   unsigned long long* bmk = (unsigned long long*)(sc + 2 * GBK);
   unsigned long long* bmp = bmk + NBK;
   unsigned long long* bmd = bmp + NBK;
-  static_assert(2 * GBK + 3 * NBK <= FIN_CAP, "finisher scratch");
-  bmk[t] = 0ull;
-  bmp[t] = 0ull;
-  bmd[t] = 0ull;
-  if (t < 6) s_ctr[t] = (t & 1) ? INT_MAX : 0;
-  uint64_t kmax = 0ull, kmin = ~0ull;
+  // each thread's entries (j = t + i WG, the mapping every pass below
+  // keeps): their probabilities and kept flags, read only by this thread
+  // until a barrier
   for (int j = t; j < E; j += WG) {
-    const uint64_t k = skey[j];
-    sv[j] = exp64_neg((key2d(k) - M) * invT, tab) / S;     // within 1 ulp, as exp
+    sv[j] = exp64_neg((key2d(skey[j]) - M) * invT, tab) / S;   // within 1 ulp, as exp
     kf[j] = 1;
-    kmax = k > kmax ? k : kmax;
-    kmin = k < kmin ? k : kmin;
   }
-  {
-    // both extremes with one barrier: every thread reads the waves' partials
-    // (scratch of their own, not written again in this call)
-    __shared__ uint64_t s_ext[2 * NWAVE];
-    const uint64_t wx = wave_max(kmax), wn = wave_min(kmin);
-    if (lane_id() == 0) { s_ext[wave_id()] = wx; s_ext[NWAVE + wave_id()] = wn; }
-    __syncthreads();
-    kmax = 0ull;
-    kmin = ~0ull;
+  uint64_t kmax = 0ull, kmin = ~0ull;
 #pragma unroll
-    for (int w = 0; w < NWAVE; ++w) {
-      kmax = s_ext[w] > kmax ? s_ext[w] : kmax;
-      kmin = s_ext[NWAVE + w] < kmin ? s_ext[NWAVE + w] : kmin;
-    }
+  for (int w = 0; w < NWAVE; ++w) {
+    kmax = ext[w] > kmax ? ext[w] : kmax;
+    kmin = ext[NWAVE + w] < kmin ? ext[NWAVE + w] : kmin;
   }
   // value buckets: linear in the value, bucket 0 holding the largest
   const double vmax = key2d(kmax), vmin = key2d(kmin);
@@ -500,6 +486,8 @@ __device__ inline int finish_row_fast(const SampleArgs& A, int row, const cx_row
   double* sc = sv + CAP;
 
   // the loaded candidates at or above the threshold into the region list
+  // (the region's extremes taken on the way)
+  uint64_t gmax = 0ull, gmin = ~0ull;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int g = r * WG + t;
@@ -507,6 +495,7 @@ __device__ inline int finish_row_fast(const SampleArgs& A, int row, const cx_row
     const bool p = s < nsp && g - s * C < st[s].ncand && c[r].key >= thr64;
     const int pos = wave_append_slot(p, &f_n);
     if (p && pos < CAP) { skey[pos] = c[r].key; sidx[pos] = c[r].idx; saux[pos] = 0; }
+    if (p) { gmax = c[r].key > gmax ? c[r].key : gmax; gmin = c[r].key < gmin ? c[r].key : gmin; }
   }
   // a slice holding more than C candidates (a flood of ties past the
   // threshold): the rest, slice by slice
@@ -521,7 +510,22 @@ __device__ inline int finish_row_fast(const SampleArgs& A, int row, const cx_row
       const bool p = e < n && cc.key >= thr64;
       const int pos = wave_append_slot(p, &f_n);
       if (p && pos < CAP) { skey[pos] = cc.key; sidx[pos] = cc.idx; saux[pos] = 0; }
+      if (p) { gmax = cc.key > gmax ? cc.key : gmax; gmin = cc.key < gmin ? cc.key : gmin; }
     }
+  }
+  // the waves' extremes and the cuts' cleared buckets, for finish_bucketed,
+  // with this barrier (the buckets lie past the region and its values)
+  __shared__ uint64_t f_ext[2 * NWAVE];
+  __shared__ int f_ctr[6];
+  {
+    const uint64_t wx = wave_max(gmax), wn = wave_min(gmin);
+    if (lane_id() == 0) { f_ext[wave_id()] = wx; f_ext[NWAVE + wave_id()] = wn; }
+    static_assert(2 * GBK + 3 * NBK <= FIN_CAP, "finisher scratch");
+    unsigned long long* bm0 = (unsigned long long*)(sc + 2 * GBK);
+    bm0[t] = 0ull;
+    bm0[NBK + t] = 0ull;
+    bm0[2 * NBK + t] = 0ull;
+    if (t < 6) f_ctr[t] = (t & 1) ? INT_MAX : 0;
   }
   __syncthreads();
   int E = f_n;
@@ -534,6 +538,8 @@ __device__ inline int finish_row_fast(const SampleArgs& A, int row, const cx_row
     uint64_t thr2 = kk + 1;
     if (t == 0) f_n = 0;
     __syncthreads();
+    gmax = 0ull;
+    gmin = ~0ull;
     for (int s = 0; s < nsp; ++s) {
       const Cand* cs = A.cands + ((size_t)row * nsp + s) * CAPS;
       const int n = st[s].ncand;
@@ -546,8 +552,11 @@ __device__ inline int finish_row_fast(const SampleArgs& A, int row, const cx_row
         const bool p = e < n && c.key >= thr2;
         const int pos = wave_append_slot(p, &f_n);
         if (p && pos < CAP) { skey[pos] = c.key; sidx[pos] = c.idx; saux[pos] = 0; }
+        if (p) { gmax = c.key > gmax ? c.key : gmax; gmin = c.key < gmin ? c.key : gmin; }
       }
     }
+    const uint64_t wx = wave_max(gmax), wn = wave_min(gmin);
+    if (lane_id() == 0) { f_ext[wave_id()] = wx; f_ext[NWAVE + wave_id()] = wn; }
     __syncthreads();
     E = f_n;
     region_incomplete_after_shrink = true;
@@ -556,7 +565,7 @@ __device__ inline int finish_row_fast(const SampleArgs& A, int row, const cx_row
   const bool region_all = region_all_pre && !region_incomplete_after_shrink;
   {
     const int rb = finish_bucketed(A, row, P, skey, sidx, saux, sv, sc, E, region_all, M, invT, S,
-                                   tol, exact, red_d, red_i, f_tab);
+                                   tol, exact, red_d, red_i, f_tab, f_ext, f_ctr);
     if (rb != FIN_SORTED) return rb;
   }
   // a cut's bucket overflowed (near-equal values): sort the region instead
