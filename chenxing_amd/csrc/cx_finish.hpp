@@ -444,37 +444,44 @@ __device__ inline int finish_row_fast(const SampleArgs& A, int row, const cx_row
   }
 
   const double invT = 1.0 / P.temperature;
-  const bool mnan = row0_reduce(lin && me.m != me.m ? 1 : 0, OpOr()) != 0;
-  const double M = row0_reduce(lin && me.m == me.m ? me.m : -__builtin_inf(), OpMax());
-  const double f = lin ? exp((me.m - M) * invT) : 0.0;       // slice s's sums to M
-  double S = row0_reduce(lin && me.s != 0.0 ? me.s * f : 0.0, OpAdd());
   const uint32_t tau = row0_reduce(lin ? me.tau : 1u, OpMax());
-  double tol = row0_reduce(lin && me.tol > TOL_S ? me.tol : TOL_S, OpMax());
-  bool exact = S_exact > 0.0;
-  if (exact) {
-    S = S_exact;
-  } else if (flags & SF_EXACT) {
-    // the slices' fp64 sums (sliced top-p rows), when every slice has one:
-    // S = sum over slices of sx_s exp((m_s - M) / T), exact when every
-    // slice's is, else within the slices' bounds (split sums)
-    const bool mx = lin && (me.flags & SF_EXACT);
-    const bool allx = row0_reduce(lin && !mx ? 1 : 0, OpOr()) == 0;
-    const double v = mx && me.sx != 0.0 ? me.sx * f : 0.0;
-    const double Sx = row0_reduce(v, OpAdd());
-    const double Bx = row0_reduce((double)(mx ? me.sxtol : 0.0f) * v, OpAdd());
-    if (allx && Sx > 0.0 && Sx < __builtin_inf()) {
-      S = Sx;
-      if (Bx == 0.0) exact = true;
-      else tol = Bx / Sx * 1.000001 + 1e-15;
+  // Tie floods, typical-p and a possible P**(1/T) underflow (ln V / T >
+  // 740) go to the multi-pass kernel; so do degenerate sums (below, once
+  // wave 0 has taken them).
+  if ((flags & SF_OVERFLOW) || P.typical_p < 1.0 || A.logV * invT > 740.0) return FIN_PENDING;
+  // The row's maximum and normaliser: wave 0 alone, after its share of the
+  // gather below (the others need only tau), lane s of row 0 taking slice s.
+  __shared__ double f_sc[3];
+  __shared__ int f_sf[2];
+  auto row_sums = [&]() {
+    const bool mnan = row0_reduce(lin && me.m != me.m ? 1 : 0, OpOr()) != 0;
+    const double M = row0_reduce(lin && me.m == me.m ? me.m : -__builtin_inf(), OpMax());
+    const double f = lin ? exp((me.m - M) * invT) : 0.0;     // slice s's sums to M
+    double S = row0_reduce(lin && me.s != 0.0 ? me.s * f : 0.0, OpAdd());
+    double tol = row0_reduce(lin && me.tol > TOL_S ? me.tol : TOL_S, OpMax());
+    bool exact = S_exact > 0.0;
+    if (exact) {
+      S = S_exact;
+    } else if (flags & SF_EXACT) {
+      // the slices' fp64 sums (sliced top-p rows), when every slice has one:
+      // S = sum over slices of sx_s exp((m_s - M) / T), exact when every
+      // slice's is, else within the slices' bounds (split sums)
+      const bool mx = lin && (me.flags & SF_EXACT);
+      const bool allx = row0_reduce(lin && !mx ? 1 : 0, OpOr()) == 0;
+      const double v = mx && me.sx != 0.0 ? me.sx * f : 0.0;
+      const double Sx = row0_reduce(v, OpAdd());
+      const double Bx = row0_reduce((double)(mx ? me.sxtol : 0.0f) * v, OpAdd());
+      if (allx && Sx > 0.0 && Sx < __builtin_inf()) {
+        S = Sx;
+        if (Bx == 0.0) exact = true;
+        else tol = Bx / Sx * 1.000001 + 1e-15;
+      }
     }
-  }
-  // Degenerate rows (NaN / +inf / all -inf), tie floods, typical-p and a
-  // possible P**(1/T) underflow (ln V / T > 740) go to the multi-pass kernel.
-  if (mnan || !(S > 0.0) || !(S < __builtin_inf()) ||
-      (flags & (SF_OVERFLOW | (exact ? 0 : SF_INEXACT))) || P.typical_p < 1.0 ||
-      A.logV * invT > 740.0) {
-    return FIN_PENDING;
-  }
+    if (lane_id() == 0) {
+      f_sc[0] = M; f_sc[1] = S; f_sc[2] = tol;
+      f_sf[0] = mnan ? 1 : 0; f_sf[1] = exact ? 1 : 0;
+    }
+  };
   bool region_incomplete_after_shrink = false;
   const bool region_all_pre = tau <= 1u;
   const uint64_t thr64 = region_all_pre ? 0ull : d2key((double)key2f(tau));
@@ -513,6 +520,7 @@ __device__ inline int finish_row_fast(const SampleArgs& A, int row, const cx_row
       if (p) { gmax = cc.key > gmax ? cc.key : gmax; gmin = cc.key < gmin ? cc.key : gmin; }
     }
   }
+  if (wave_id() == 0) row_sums();
   // the waves' extremes and the cuts' cleared buckets, for finish_bucketed,
   // with this barrier (the buckets lie past the region and its values)
   __shared__ uint64_t f_ext[2 * NWAVE];
@@ -528,6 +536,11 @@ __device__ inline int finish_row_fast(const SampleArgs& A, int row, const cx_row
     if (t < 6) f_ctr[t] = (t & 1) ? INT_MAX : 0;
   }
   __syncthreads();
+  const double M = f_sc[0], S = f_sc[1], tol = f_sc[2];
+  const bool exact = f_sf[1] != 0;
+  // degenerate rows (NaN / +inf / all -inf) and inexact sums
+  if (f_sf[0] || !(S > 0.0) || !(S < __builtin_inf()) || (!exact && (flags & SF_INEXACT)))
+    return FIN_PENDING;
   int E = f_n;
   if (E > CAP) {
     // Shrink the region to the CAP largest candidates (strictly above the
