@@ -714,8 +714,10 @@ __device__ __forceinline__ void stream_stoch(__amdgpu_buffer_rsrc_t rs,
     const int cnn = cn < nch ? __builtin_amdgcn_readfirstlane(next_chunk(chunk_ctr)) : nch;
     load_chunk<BF16>(rs, cnn, b);      // past the slice: zeros, never consumed
     // after the refill, so both chunks are in flight while the wave
-    // publishes (a publish is a few hundred instructions)
-    if ((it == 1 || it == 3) && fresh) {
+    // publishes (a publish is a few hundred instructions); not once the
+    // slice's chunks are all handed out (a raised threshold would filter
+    // only the chunks already in flight)
+    if ((it == 1 || it == 3) && fresh && cnn < nch) {
       publish(ck, krow, pub_r, slots, w_pub, wb.shared);
       raise_tau(wb, lds_load(wb.shared));
       fresh = false;
