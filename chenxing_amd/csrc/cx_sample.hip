@@ -1367,13 +1367,17 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   }
 
   // ---- per wave, after its stream: its region entries into the shared
-  // list, its penalty corrections (with the penalised values at or above
-  // its threshold), its sums and state for the combination
+  // list (the one-wave top-k finish's, so only for its rows), its penalty
+  // corrections (with the penalised values at or above its threshold), its
+  // sums and state for the combination
+  // Top-k rows the rank-parallel finish can take (static conditions).
+  const bool lean_static = single && P.top_k > 0 && P.top_k <= 64 && P.typical_p >= 1.0 &&
+                           !A.out_probs && A.logV * (1.0 / P.temperature) <= 740.0;
   raise_tau(wb, lds_load(wb.shared));
   // lanes read below the buffer entries other lanes of the wave wrote (in
   // order on the hardware; the barrier keeps the compiler from hoisting)
   __builtin_amdgcn_wave_barrier();
-  {
+  if (lean_static) {
     const int n = wb.n;
     for (int e = lane_id(); e < n; e += 64) {
       const uint32_t k = wb.key[e];
@@ -1407,9 +1411,6 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   sl = wave_reduce(sl, OpAdd());
   const uint32_t kmx_w = wave_reduce(ck, OpMax());
   const int fl = wave_reduce(st.s != st.s ? 1 : 0, OpOr());
-  // Top-k rows the rank-parallel finish can take (static conditions).
-  const bool lean_static = single && P.top_k > 0 && P.top_k <= 64 && P.typical_p >= 1.0 &&
-                           !A.out_probs && A.logV * (1.0 / P.temperature) <= 740.0;
   if (krow <= 64 && !lean_static) publish_top(ck, NSLOT, lslots + NSLOT * wave_id());
   if (lane_id() == 0) {
     w_s[wave_id()] = sl;
