@@ -1098,6 +1098,7 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   __shared__ uint32_t slots[4 * NWAVE];
   __shared__ int s_chunk;
   __shared__ int s_cnt;
+  __shared__ int s_rcnt;                      // region entries written (general rows)
   __shared__ LeanLds s_lean;
 
   __shared__ int s_nd;
@@ -1177,7 +1178,9 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   X.nbw = (hi - lo + 31) >> 5;
   X.ns = pen_on ? A.ns : 0;
   X.ns_log2 = A.ns_log2;
-  if (t == 0) { sP = P0; s_shared = 1u; s_chunk = 2 * NWAVE; s_cnt = 0; s_nd = 0; s_gctr = 0; }
+  if (t == 0) {
+    sP = P0; s_shared = 1u; s_chunk = 2 * NWAVE; s_cnt = 0; s_rcnt = 0; s_nd = 0; s_gctr = 0;
+  }
   if (t < LEAN_CAP) { s_lean.rv[t] = 0; s_lean.ri[t] = 0; }
   if (t < NWAVE) { w_pub[t] = 0u; w_cnt[t] = 0; }
   if (t < 4 * NWAVE) slots[t] = 0u;
@@ -1418,6 +1421,7 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
     w_tau[wave_id()] = wb.tau;
     w_kmx[wave_id()] = kmx_w;
     w_fl[wave_id()] = fl | (wb.overflow ? 2 : 0) | (wb.lossy ? 4 : 0);
+    w_cnt[wave_id()] = wb.n;
   }
   __syncthreads();
   const int lw = lane_id() & 15;       // lane w of row 0 reads wave w's record
@@ -1563,10 +1567,18 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   // entries at or above it (the same bound the waves' own compactions to kw
   // entries gave, in one pass and one barrier).  The bins are the top-k
   // finish's rank counters, zeroed at the start and unused on this path.
-  {
+  // Whole-row buffers holding no more than the cap in all (most top-k 100
+  // rows of a 256000-entry vocabulary) need no histogram: T is Tf.  A
+  // slice's buffers nearly always exceed it, so the sliced launch does not
+  // test.
+  const int cap = NWAVE * wb.kw;
+  const uint32_t tlo = Tf > 1u ? Tf : 1u;
+  if (!EXACT && row0_reduce(w_cnt[lw], OpAdd()) <= cap) {
+    Tf = tlo;
+  } else {
     static_assert(2 * LEAN_CAP == 512, "histogram bins");
     CX_LDS int* const bins = to_lds(&s_lean.rv[0]);     // rv, then ri: 512 counters
-    const uint32_t lo = Tf > 1u ? Tf : 1u;
+    const uint32_t lo = tlo;
     const uint32_t d = kmx > lo ? kmx - lo : 0u;
     const int sh = d ? max(0, 23 - (int)__clz(d)) : 0;  // d >> sh < 512
     const uint32_t base = lo >> sh;
@@ -1576,11 +1588,9 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
       if (k >= lo) __hip_atomic_fetch_add(bins + min((int)((k >> sh) - base), 511), 1,
                                           CX_RELAXED_WG);
     }
-    if (t == 0) s_cnt = 0;
     __syncthreads();
     // every wave: lane l holds bins 8l .. 8l + 7; the lowest bin b whose
     // suffix count is at most the cap
-    const int cap = NWAVE * wb.kw;
     int cb[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) cb[j] = lds_load(bins + 8 * lane_id() + j);
@@ -1609,7 +1619,7 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
     const double xp = penalise(X.hval[s], (int)(hw & 0xFFFu), P);
     const uint64_t k64 = d2key(xp);
     if (k64 >= thr64 && xp == xp) {
-      const int pos = atomicAdd(&s_cnt, 1);
+      const int pos = atomicAdd(&s_rcnt, 1);
       mycand[pos].key = k64;
       mycand[pos].idx = (int32_t)(hw >> 12);
     }
@@ -1620,7 +1630,7 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
       const bool keep = e < n && wb.key[e] >= Tf;
       const uint64_t b = ballot(keep);
       int base = 0;
-      if (lane_id() == 0 && b) base = atomicAdd(&s_cnt, (int)__popcll(b));
+      if (lane_id() == 0 && b) base = atomicAdd(&s_rcnt, (int)__popcll(b));
       base = __shfl(base, 0);
       if (keep) {
         const int pos = base + lanes_below(b);
@@ -1639,7 +1649,7 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
     my->s = EXACT && exs ? Sx : (sum_ok ? Ss * exp2(Rb - Ms * kc) : Ss);
     my->tol = EXACT && exs ? xtol * 1.001 : tol;
     my->best_v = 0; my->best_i = INT_MAX; my->nan_i = INT_MAX;
-    my->tau = Tf; my->ncand = s_cnt;
+    my->tau = Tf; my->ncand = s_rcnt;
     my->flags = (ovf ? SF_OVERFLOW : 0) | ((EXACT && exs ? xok : sum_ok) ? 0 : SF_INEXACT) |
                 (xok ? SF_EXACT : 0);
   }
