@@ -1097,7 +1097,7 @@ __global__ __launch_bounds__(WG) void sample_kernel(SampleArgs A) {
   __shared__ uint32_t w_pub[NWAVE];
   __shared__ uint32_t slots[4 * NWAVE];
   __shared__ int s_chunk;
-  __shared__ int s_cnt;
+  __shared__ int s_cnt;                       // the one-wave top-k finish's list (pen_correct's too)
   __shared__ int s_rcnt;                      // region entries written (general rows)
   __shared__ LeanLds s_lean;
 
