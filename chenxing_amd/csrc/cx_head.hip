@@ -58,8 +58,10 @@ struct HeadArgs {
   float* out_logits;        // nullable [B, V] (verification)
 };
 
+// 16 bytes of head weights: a plain load (the non-temporal form measured
+// 0.5 us slower over the 1 GB at B=16)
 __device__ __forceinline__ u32x4 ld16(const uint16_t* p) {
-  return __builtin_nontemporal_load((const u32x4*)p);
+  return *(const u32x4*)p;
 }
 
 // The 64-bit argmax key of logit x at vocab id v.
