@@ -454,11 +454,14 @@ __device__ __forceinline__ double sign_margin(const SeqState& q, float T) {
 }
 
 // Eight consecutive logits [e0, e0 + 8) of a row (zeros past hi), with two
-// 16-byte loads when they are whole and aligned.
+// 16-byte loads when they are whole and aligned.  Plain loads: the draw reads
+// one sub-chunk of the same row pair again, from the L2 (1 us off the verify
+// step against non-temporal ones; the stats pass keeps them: 4 us slower
+// without).
 __device__ __forceinline__ void load8(const float* row, int e0, int hi, float (&x)[8]) {
   if (e0 + 8 <= hi && (((uintptr_t)(row + e0)) & 15) == 0) {
-    const f32x4 a = __builtin_nontemporal_load((const f32x4*)(row + e0));
-    const f32x4 c = __builtin_nontemporal_load((const f32x4*)(row + e0) + 1);
+    const f32x4 a = *((const f32x4*)(row + e0));
+    const f32x4 c = *((const f32x4*)(row + e0) + 1);
     x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
     x[4] = c.x; x[5] = c.y; x[6] = c.z; x[7] = c.w;
   } else {
